@@ -1,0 +1,132 @@
+// Shared definitions of the MI355X (gfx950) quantized matrix-product library.
+//
+// Device layout of a table (the device mirror of a fusor-ai Table, tensor.rs:1-9). The host hands
+// over the reference bytes (quad-major codes, then f32 scales); the upload rewrites the codes so
+// that every kernel reads a row's codes of one 32-input block contiguously:
+//   * quad q (rows 4q..4q+3), block b: a "quad block" of 4 row-blocks, [lane][codes];
+//   * Q7b32 / Q8b32: 32 signed int8 levels per row-block (Q7b32 stores u - 64, so the
+//     correction -64·Σa is folded into the levels: Σ(u-64)·a == corr + Σu·a exactly);
+//   * Q4b32: 16 bytes per row-block, byte i holding code i in its low nibble and code i + 16 in
+//     its high nibble, offset-binary as the reference stores them (u = q + 8);
+//   * scales: unchanged, f32 at ((q·G + g)·4 + lane).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/fusor_gpu.h"
+
+namespace fg {
+
+constexpr int kBlock = 32;
+constexpr int kQuad = 4;
+constexpr int kTernaryGroup = 128;
+
+inline int group_of(int dtype) { return dtype == FG_T2B128 ? kTernaryGroup : kBlock; }
+inline int zero_point_of(int dtype)
+{
+    switch (dtype) {
+    case FG_Q7B32: return 64;
+    case FG_Q4B32: return 8;
+    case FG_T2B128: return 1;
+    default: return 0;
+    }
+}
+inline int codes_per_byte(int dtype) { return dtype == FG_Q4B32 ? 2 : dtype == FG_T2B128 ? 4 : 1; }
+inline bool is_quantized(int dtype) { return dtype >= FG_Q7B32 && dtype <= FG_Q8B32; }
+// Bytes of one quad block in the reference layout (tensor.rs:129): 128 / 64 / 32.
+inline size_t quad_bytes(int dtype) { return size_t(kQuad * kBlock / codes_per_byte(dtype)); }
+inline size_t padded_values(size_t rows, size_t cols) { return (rows + kQuad - 1) / kQuad * kQuad * cols; }
+
+}  // namespace fg
+
+struct fg_table {
+    int dtype;
+    size_t rows, cols;
+    size_t quads, blocks, groups;
+    int8_t *codes;   // device layout, quads * blocks * quad_bytes bytes
+    float *scales;   // quads * groups * 4
+    size_t code_bytes;
+};
+
+namespace fg {
+
+// ------------------------------------------------------------------ errors (host side)
+
+int set_error(int code, const std::string &message);
+int check_hip(hipError_t e, const char *what);
+
+#define FG_HIP(call)                                                          \
+    do {                                                                      \
+        hipError_t fg_e_ = (call);                                            \
+        if (fg_e_ != hipSuccess) return ::fg::check_hip(fg_e_, #call);        \
+    } while (0)
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------------ device helpers
+
+__device__ __forceinline__ int dot4(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
+
+// The partner lane's value in pairs (lane ^ 1), through DPP.
+__device__ __forceinline__ int xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+
+// Activation quantization of one value at scale d (scalar.rs:57-66): ties-to-even rounding of the
+// IEEE quotient, clamped to ±127 in float, NaN to 0 (Rust's saturating cast).
+__device__ __forceinline__ int quantize_level(float x, float d)
+{
+    float r = __builtin_rintf(x / d);
+    if (r != r) return 0;
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return int(r);
+}
+
+// `extreme == 0 ? 1 : extreme / level` (quant.rs:126-128).
+__device__ __forceinline__ float group_scale(float extreme, float level) { return extreme == 0.0f ? 1.0f : extreme / level; }
+
+// Pack four int8 levels into one dword, lowest first.
+__device__ __forceinline__ int pack4(int a, int b, int c, int d)
+{
+    return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | ((d & 0xff) << 24);
+}
+
+// Offset-binary nibbles (u in [0,15]) of a dword to signed levels u - 8, byte-wise without
+// borrows: (u + 0x78) ^ 0x80 == u - 8 as an int8.
+__device__ __forceinline__ int nibbles_signed(int packed_nibbles)
+{
+    return ((packed_nibbles & 0x0F0F0F0F) + 0x78787878) ^ int(0x80808080u);
+}
+
+}  // namespace fg
+
+// Host-side launchers shared between translation units.
+namespace fg {
+int launch_relayout(const uint8_t *ref_codes, fg_table *t, hipStream_t s);
+int launch_unrelayout(const fg_table *t, uint8_t *ref_codes, hipStream_t s);
+int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint8_t *bytes, hipStream_t s);
+int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s);
+int launch_quantize_rows(const float *x, size_t count, int dtype, int8_t *q, float *scales, int32_t *corr,
+                         hipStream_t s);
+
+// One product: rows of int8 levels (q, scales, corrections) or f32 rows x quantized in-kernel.
+struct ProductArgs {
+    const fg_table *t;
+    const float *x;
+    const int8_t *q;
+    const float *as;
+    const int32_t *corr;
+    size_t rows;
+    size_t quad_begin, quad_end;
+    const float *bias;
+    float *out;
+    size_t ld_out;
+    int accumulate;
+    int32_t *dots;  // when set, the int32 group accumulators are written instead of out
+};
+int launch_matvec(const ProductArgs &a, hipStream_t s);
+int launch_gemm(const ProductArgs &a, hipStream_t s);
+int launch_product(const ProductArgs &a, hipStream_t s);
+}  // namespace fg

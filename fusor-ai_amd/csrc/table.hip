@@ -1,0 +1,267 @@
+// Tables on the device: the reference byte layout in and out (tensor.rs:1-9, quant.rs:89-118),
+// Tensor::encode (tensor.rs:97-143, quant.rs:143-177), Matrix::dequantize_row (tensor.rs:247-271)
+// and the activation quantizer quantize_rows (matmul.rs:233-257, arch/scalar.rs:48-66).
+#include "common.h"
+
+namespace fg {
+namespace {
+
+// Where code `input` of row `lane` sits in a reference quad block, and its shift
+// (quant.rs:89-95).
+__device__ __forceinline__ void code_position(int cpb, int lane, int input, int &byte, int &shift)
+{
+    int chunk = input >> 2, offset = input & 3;
+    int words = 8 / cpb, bits = 8 / cpb;
+    byte = (chunk % words) * 16 + lane * 4 + offset;
+    shift = bits * (chunk / words);
+}
+
+// Reference quad blocks to device quad blocks (and back with `inverse`): one thread per
+// (quad, block).
+__global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int dtype,
+                                size_t quad_blocks, int inverse)
+{
+    size_t qb = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (qb >= quad_blocks) return;
+    int cpb = dtype == FG_Q4B32 ? 2 : dtype == FG_T2B128 ? 4 : 1;
+    int qbytes = 128 / cpb;
+    int mask = 0xff >> (8 - 8 / cpb);
+    uint8_t ref[128];
+    uint8_t dev[128];
+    const uint8_t *in = src + qb * qbytes;
+    if (!inverse) {
+        for (int i = 0; i < qbytes; i++) ref[i] = in[i];
+        for (int i = 0; i < qbytes; i++) dev[i] = 0;
+        for (int lane = 0; lane < 4; lane++) {
+            for (int k = 0; k < 32; k++) {
+                int byte, shift;
+                code_position(cpb, lane, k, byte, shift);
+                int u = (ref[byte] >> shift) & mask;
+                if (dtype == FG_Q7B32) dev[lane * 32 + k] = uint8_t(int8_t(u - 64));
+                else if (dtype == FG_Q8B32) dev[lane * 32 + k] = uint8_t(u);
+                else if (dtype == FG_Q4B32) dev[lane * 16 + (k & 15)] |= uint8_t(u << (4 * (k >> 4)));
+                else dev[lane * 8 + (k & 7)] |= uint8_t(u << (2 * (k >> 3)));
+            }
+        }
+        uint8_t *out = dst + qb * qbytes;
+        for (int i = 0; i < qbytes; i++) out[i] = dev[i];
+    } else {
+        for (int i = 0; i < qbytes; i++) dev[i] = in[i];
+        for (int i = 0; i < qbytes; i++) ref[i] = 0;
+        for (int lane = 0; lane < 4; lane++) {
+            for (int k = 0; k < 32; k++) {
+                int u;
+                if (dtype == FG_Q7B32) u = int(int8_t(dev[lane * 32 + k])) + 64;
+                else if (dtype == FG_Q8B32) u = dev[lane * 32 + k];
+                else if (dtype == FG_Q4B32) u = (dev[lane * 16 + (k & 15)] >> (4 * (k >> 4))) & 15;
+                else u = (dev[lane * 8 + (k & 7)] >> (2 * (k >> 3))) & 3;
+                int byte, shift;
+                code_position(cpb, lane, k, byte, shift);
+                ref[byte] |= uint8_t(u << shift);
+            }
+        }
+        uint8_t *out = dst + qb * qbytes;
+        for (int i = 0; i < qbytes; i++) out[i] = ref[i];
+    }
+}
+
+// Rust's saturating float casts (NaN to 0).
+__device__ __forceinline__ int sat_i8(float v) { return v != v ? 0 : v >= 127.0f ? 127 : v <= -128.0f ? -128 : int(v); }
+__device__ __forceinline__ int sat_u8(float v) { return v != v ? 0 : v >= 255.0f ? 255 : v <= 0.0f ? 0 : int(v); }
+__device__ __forceinline__ int sat_i32(float v)
+{
+    return v != v ? 0 : v >= 2147483648.0f ? 2147483647 : v <= -2147483648.0f ? int(0x80000000u) : int(v);
+}
+// f32::clamp keeps NaN.
+__device__ __forceinline__ float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// One group of a row to codes; returns its scale (quant.rs:143-177, Q8b32 extension).
+__device__ float quantize_group(int dtype, const float *x, int n, uint8_t *codes)
+{
+    if (dtype == FG_Q4B32) {
+        float extreme = 0.0f;
+        for (int i = 0; i < n; i++)
+            if (fabsf(x[i]) > fabsf(extreme)) extreme = x[i];
+        float scale = group_scale(extreme, -8.0f);
+        for (int i = 0; i < n; i++) codes[i] = uint8_t(sat_u8(clampf(__builtin_rintf(x[i] / scale) + 8.0f, 0.0f, 15.0f)));
+        return scale;
+    }
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++) amax = fmaxf(amax, fabsf(x[i]));
+    if (dtype == FG_T2B128) {
+        float scale = group_scale(amax, 1.0f);
+        for (int i = 0; i < n; i++) codes[i] = uint8_t(sat_i32(clampf(__builtin_rintf(x[i] / scale), -1.0f, 1.0f)) + 1);
+        return scale;
+    }
+    float level_max = dtype == FG_Q7B32 ? 63.0f : 127.0f;
+    float scale = group_scale(amax, level_max);
+    for (int i = 0; i < n; i++) {
+        int level = sat_i8(__builtin_rintf(x[i] / scale));
+        if (dtype == FG_Q7B32) {
+            level = level < -63 ? -63 : (level > 63 ? 63 : level);
+            codes[i] = uint8_t(level + 64);
+        } else {
+            level = level < -127 ? -127 : level;
+            codes[i] = uint8_t(int8_t(level));
+        }
+    }
+    return scale;
+}
+
+// Tensor::encode: one thread per (quad, group) writes the group's blocks of all four rows and
+// their scales, padding rows as zero codes and zero scales (tensor.rs:83-88,124-143).
+__global__ void encode_kernel(int dtype, size_t rows, size_t cols, const float *__restrict__ values,
+                              uint8_t *__restrict__ bytes, size_t quant_len, size_t quads)
+{
+    int group = dtype == FG_T2B128 ? 128 : 32;
+    size_t groups = cols / group, blocks = cols / 32;
+    size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= quads * groups) return;
+    size_t quad = id / groups, g = id % groups;
+    int cpb = dtype == FG_Q4B32 ? 2 : dtype == FG_T2B128 ? 4 : 1;
+    int qbytes = 128 / cpb;
+    float *scales = reinterpret_cast<float *>(bytes + quant_len);
+    int bpg = group / 32;
+    uint8_t quadblock[4][128];
+    for (int b = 0; b < bpg; b++)
+        for (int i = 0; i < qbytes; i++) quadblock[b][i] = 0;
+    for (int lane = 0; lane < 4; lane++) {
+        size_t row = quad * 4 + lane;
+        uint8_t codes[128];
+        float scale = 0.0f;
+        if (row < rows) {
+            scale = quantize_group(dtype, values + row * cols + g * group, group, codes);
+        } else {
+            for (int i = 0; i < group; i++) codes[i] = 0;
+        }
+        scales[(quad * groups + g) * 4 + lane] = scale;
+        for (int b = 0; b < bpg; b++) {
+            for (int k = 0; k < 32; k++) {
+                int byte, shift;
+                code_position(cpb, lane, k, byte, shift);
+                quadblock[b][byte] |= uint8_t(codes[b * 32 + k] << shift);
+            }
+        }
+    }
+    for (int b = 0; b < bpg; b++) {
+        uint8_t *out = bytes + (quad * blocks + g * bpg + b) * qbytes;
+        for (int i = 0; i < qbytes; i++) out[i] = quadblock[b][i];
+    }
+}
+
+// The signed level of code k of a device row-block.
+__device__ __forceinline__ int device_level(int dtype, const int8_t *quadblock, int lane, int k)
+{
+    const uint8_t *u = reinterpret_cast<const uint8_t *>(quadblock);
+    switch (dtype) {
+    case FG_Q4B32: return int((u[lane * 16 + (k & 15)] >> (4 * (k >> 4))) & 15) - 8;
+    case FG_T2B128: return int((u[lane * 8 + (k & 7)] >> (2 * (k >> 3))) & 3) - 1;
+    default: return int(quadblock[lane * 32 + k]);
+    }
+}
+
+// out[k] = scale · (float)level (quant.rs:80-85), one thread per value.
+__global__ void dequantize_row_kernel(const int8_t *__restrict__ codes, const float *__restrict__ scales, int dtype,
+                                      size_t row, size_t cols, float *__restrict__ out)
+{
+    size_t k = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= cols) return;
+    int group = dtype == FG_T2B128 ? 128 : 32;
+    size_t blocks = cols / 32, groups = cols / group;
+    size_t quad = row / 4;
+    int lane = int(row % 4);
+    size_t b = k / 32;
+    int qbytes = dtype == FG_Q4B32 ? 64 : dtype == FG_T2B128 ? 32 : 128;
+    int level = device_level(dtype, codes + (quad * blocks + b) * qbytes, lane, int(k % 32));
+    float scale = scales[(quad * groups + b / (group / 32)) * 4 + lane];
+    out[k] = scale * float(level);
+}
+
+// quantize_rows: `lanes` threads per group (8 for groups of 32, 32 for groups of 128), four
+// values per thread. The group's absmax is a max over its values (order-free, NaN ignored as
+// f32::max does); its scale amax/127 by IEEE division; every level rounds ties to even.
+template <int LANES>
+__global__ void quantize_rows_kernel(const float *__restrict__ x, size_t groups, int zp, int8_t *__restrict__ q,
+                                     float *__restrict__ scales, int32_t *__restrict__ corr)
+{
+    size_t t = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    size_t g = t / LANES;
+    int sub = int(t % LANES);
+    bool active = g < groups;
+    float4 v = active ? reinterpret_cast<const float4 *>(x)[g * LANES + sub] : make_float4(0, 0, 0, 0);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(0.0f, amax);
+    for (int m = 1; m < LANES; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    float d = group_scale(amax, 127.0f);
+    int l0 = quantize_level(v.x, d), l1 = quantize_level(v.y, d), l2 = quantize_level(v.z, d), l3 = quantize_level(v.w, d);
+    int sum = l0 + l1 + l2 + l3;
+    for (int m = 1; m < LANES; m <<= 1) sum += __shfl_xor(sum, m, 64);
+    if (!active) return;
+    reinterpret_cast<int *>(q)[g * LANES + sub] = pack4(l0, l1, l2, l3);
+    if (sub == 0) {
+        scales[g] = d;
+        corr[g] = -zp * sum;
+    }
+}
+
+}  // namespace
+
+int launch_relayout(const uint8_t *ref_codes, fg_table *t, hipStream_t s)
+{
+    size_t n = t->quads * t->blocks;
+    if (n == 0) return FG_OK;
+    unsigned grid = unsigned((n + 255) / 256);
+    relayout_kernel<<<grid, 256, 0, s>>>(ref_codes, reinterpret_cast<uint8_t *>(t->codes), t->dtype, n, 0);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+int launch_unrelayout(const fg_table *t, uint8_t *ref_codes, hipStream_t s)
+{
+    size_t n = t->quads * t->blocks;
+    if (n == 0) return FG_OK;
+    unsigned grid = unsigned((n + 255) / 256);
+    relayout_kernel<<<grid, 256, 0, s>>>(reinterpret_cast<const uint8_t *>(t->codes), ref_codes, t->dtype, n, 1);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint8_t *bytes, hipStream_t s)
+{
+    size_t quads = (rows + 3) / 4;
+    size_t groups = cols / size_t(group_of(dtype));
+    size_t quant_len = padded_values(rows, cols) / size_t(codes_per_byte(dtype));
+    size_t n = quads * groups;
+    if (n == 0) return FG_OK;
+    encode_kernel<<<unsigned((n + 127) / 128), 128, 0, s>>>(dtype, rows, cols, values, bytes, quant_len, quads);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s)
+{
+    if (t->cols == 0) return FG_OK;
+    dequantize_row_kernel<<<unsigned((t->cols + 255) / 256), 256, 0, s>>>(t->codes, t->scales, t->dtype, row, t->cols, out);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+int launch_quantize_rows(const float *x, size_t count, int dtype, int8_t *q, float *scales, int32_t *corr,
+                         hipStream_t s)
+{
+    int group = group_of(dtype);
+    size_t groups = count / size_t(group);
+    if (groups == 0) return FG_OK;
+    int zp = zero_point_of(dtype);
+    if (group == 32) {
+        size_t threads = groups * 8;
+        quantize_rows_kernel<8><<<unsigned((threads + 255) / 256), 256, 0, s>>>(x, groups, zp, q, scales, corr);
+    } else {
+        size_t threads = groups * 32;
+        quantize_rows_kernel<32><<<unsigned((threads + 255) / 256), 256, 0, s>>>(x, groups, zp, q, scales, corr);
+    }
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+}  // namespace fg

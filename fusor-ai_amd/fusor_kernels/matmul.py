@@ -1,0 +1,120 @@
+"""Activation quantization and the quantized product (matmul.rs), on the GPU.
+
+`quantize_rows`, `QuantizedRows.input` and `matmul` keep the reference's names and argument
+meaning; activations and outputs are device tensors (torch, float32 / int8 / int32).
+"""
+
+import ctypes
+
+from . import _lib
+from ._lib import FgInput, ShapeError, check, lib, ptr, stream_handle
+from .tensor import QUAD, QuantFormat
+
+ROWS_PER_CALL = 64  # matmul.rs:407
+
+
+def quantize_rows(x, fmt, quants, scales, corrections):
+    """quantize_rows (matmul.rs:233-257): `x` (device f32), whole groups of `fmt`, to int8 levels
+    with each group's scale (absmax / 127) and correction (-zero_point * Σq)."""
+    fmt = QuantFormat(fmt)
+    check(lib().fg_quantize_rows(ptr(x), x.numel(), int(fmt), ptr(quants), ptr(scales), ptr(corrections),
+                                 stream_handle()))
+
+
+class Quantized:
+    """matmul.rs:104-112"""
+
+    def __init__(self, fmt, quants, scales, corrections):
+        self.format, self.quants, self.scales, self.corrections = QuantFormat(fmt), quants, scales, corrections
+
+
+class Input:
+    """matmul.rs:114-147: f32 rows (quantized inside the product) or rows quantized for a format."""
+
+    def __init__(self, f32=None, quant=None):
+        self.f32, self.quant = f32, quant
+
+    def rows(self, width):
+        return (self.f32.numel() if self.f32 is not None else self.quant.quants.numel()) // width
+
+    def block(self, width, start, end):
+        """Input::block: rows start..end."""
+        if self.f32 is not None:
+            return Input(f32=self.f32.reshape(-1)[start * width:end * width])
+        q = self.quant
+        per_row = width // q.format.group()
+        return Input(quant=Quantized(q.format, q.quants[start * width:end * width], q.scales[start * per_row:end * per_row],
+                                     q.corrections[start * per_row:end * per_row]))
+
+    def ffi(self):
+        if self.f32 is not None:
+            return FgInput(ptr(self.f32), None, None, None)
+        q = self.quant
+        return FgInput(None, ptr(q.quants), ptr(q.scales), ptr(q.corrections))
+
+
+class QuantizedRows:
+    """matmul.rs:26-33,149-229: rows of activations quantized for one weight format, on the device."""
+
+    def __init__(self):
+        self.quants = self.scales = self.corrections = None
+
+    def input(self, weights, x):
+        """Prepares `x` (device f32, whole rows of weights.cols) as the input of `weights`."""
+        import torch
+        if x.numel() % weights.cols:
+            raise ShapeError("the input is whole rows of the weights' width")
+        fmt = weights.format
+        n = x.numel()
+        g = fmt.group()
+        self.quants = torch.empty(n, dtype=torch.int8, device=x.device)
+        self.scales = torch.empty(n // g, dtype=torch.float32, device=x.device)
+        self.corrections = torch.empty(n // g, dtype=torch.int32, device=x.device)
+        quantize_rows(x.reshape(-1), fmt, self.quants, self.scales, self.corrections)
+        return Input(quant=Quantized(fmt, self.quants, self.scales, self.corrections))
+
+
+def _check_input(weights, x):
+    if x.quant is not None and x.quant.format != weights.format:
+        raise ShapeError("the input is prepared for the weights' format")  # matmul.rs:301-304
+
+
+def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False):
+    """matmul (matmul.rs:265-276) over output columns `cols` (a range of whole quads).
+
+    Returns the device tensor [rows, len(cols)] of results; with `store`, also calls
+    store(row, first_col, [4 floats]) per row and quad, in the reference's order.
+    """
+    import torch
+    if cols.start % QUAD or cols.stop % QUAD:
+        raise ShapeError("columns in whole quads")  # matmul.rs:271-274
+    _check_input(weights, x)
+    rows = x.rows(weights.cols)
+    width = cols.stop - cols.start
+    if out is None:
+        out = torch.empty((rows, width), dtype=torch.float32, device="cuda")
+    inp = x.ffi()
+    check(lib().fg_matmul(weights.table.handle, ctypes.byref(inp), rows, cols.start, cols.stop, ptr(bias), ptr(out),
+                          out.stride(0) if out.dim() == 2 else width, _lib.FG_ACCUMULATE if accumulate else 0,
+                          stream_handle()))
+    if store is not None:
+        host = out.cpu().numpy()
+        for r in range(rows):
+            for first in range(0, width, QUAD):
+                store(r, cols.start + first, host[r, first:first + QUAD].tolist())
+    return out
+
+
+def matmul_dots(weights, x, cols):
+    """The int32 group accumulators of the same product: [rows, len(cols), groups]."""
+    import torch
+    if cols.start % QUAD or cols.stop % QUAD:
+        raise ShapeError("columns in whole quads")
+    _check_input(weights, x)
+    rows = x.rows(weights.cols)
+    groups = weights.cols // weights.format.group()
+    dots = torch.empty((rows, cols.stop - cols.start, groups), dtype=torch.int32, device="cuda")
+    inp = x.ffi()
+    check(lib().fg_matmul_dots(weights.table.handle, ctypes.byref(inp), rows, cols.start, cols.stop, ptr(dots),
+                               stream_handle()))
+    return dots

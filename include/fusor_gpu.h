@@ -1,0 +1,150 @@
+/*
+ * fusor_gpu.h — the C ABI of the MI355X (gfx950) quantized matrix-product path.
+ *
+ * These entry points are what fusor-ai's `kernels` crate (crates/kernels/src) would bind through
+ * a thin `-sys` crate so that its Rust API stays unchanged: each declaration names the reference
+ * interface it replaces (file:line, relative to the fusor-ai checkout). Plain pointers and sizes
+ * only. Pointers documented as "device" are HIP device addresses; `stream` is a hipStream_t
+ * (NULL is the null stream). Every call returns a status code (FG_OK on success); the message of
+ * the last failure on the calling thread is fg_last_error(). No call retains a caller pointer
+ * after it returns, except the table and model handles, which own their device memory.
+ *
+ * Calls are thread-safe: the reference calls the product from every thread of a team
+ * (linear.rs:113-143); concurrent calls on disjoint outputs are independent.
+ */
+#ifndef FUSOR_GPU_H
+#define FUSOR_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The reference panics on shape and format misuse (matmul.rs:271-274,301-304,
+ * 531-541; linear.rs:58-61) and returns Error::Format on construction (tensor.rs:97-104,
+ * 163-171,200-211); a binding maps FG_ERR_SHAPE / FG_ERR_FORMAT to those. */
+#define FG_OK 0
+#define FG_ERR_SHAPE 1     /* shapes or ranges that do not fit */
+#define FG_ERR_FORMAT 2    /* a data type this call does not take */
+#define FG_ERR_HIP 3       /* the HIP runtime failed */
+#define FG_ERR_NOMEM 4     /* device memory ran out */
+#define FG_ERR_ARG 5       /* a null or otherwise invalid argument */
+
+/* Data types: DType (tensor.rs:19-24). FG_Q8B32 is this library's extension: signed int8 levels
+ * in [-127, 127] (zero point 0, one byte per code) in Q7b32's quad and scale layout. */
+#define FG_F32 0
+#define FG_Q7B32 1
+#define FG_Q4B32 2
+#define FG_T2B128 3
+#define FG_Q8B32 4
+
+/* Flags of fg_matmul. */
+#define FG_ACCUMULATE 1 /* out += result: project_residual_input (linear.rs:134-143) */
+
+/* The last failure's message on this thread ("" when none). */
+const char *fg_last_error(void);
+
+/* Library version, for a binding's build check. */
+int fg_version(void);
+
+/* ----------------------------------------------------------------------------- tables */
+
+/* A quantized [rows, cols] weight matrix resident on the device: the device mirror of a Table
+ * (tensor.rs:195-232), created once per Table and freed on drop. */
+typedef struct fg_table fg_table;
+
+/* Table::new + upload (tensor.rs:200-211). `bytes` (host) are the Tensor's bytes in the
+ * reference layout: quad-major codes, then f32 scales (tensor.rs:1-9). `len` must equal the
+ * dtype's byte length for the shape (tensor.rs:39-51). */
+int fg_table_create(const void *bytes, size_t len, int dtype, size_t rows, size_t cols, void *stream,
+                    fg_table **out);
+/* The same from device bytes in the reference layout. */
+int fg_table_create_device(const void *bytes, size_t len, int dtype, size_t rows, size_t cols,
+                           void *stream, fg_table **out);
+int fg_table_free(fg_table *table);
+/* Matrix{rows, cols} and the DType of a table (tensor.rs:67-71). */
+int fg_table_shape(const fg_table *table, int *dtype, size_t *rows, size_t *cols);
+/* The table's bytes back in the reference layout (device `bytes`, fg_table_byte_len long). */
+size_t fg_table_byte_len(int dtype, size_t rows, size_t cols);
+int fg_table_read(const fg_table *table, void *bytes, void *stream);
+
+/* Tensor::encode of a quantized [rows, cols] matrix (tensor.rs:97-143, quant.rs:143-177):
+ * device f32 `values` (row-major) to device `bytes` (fg_table_byte_len long) in the reference
+ * layout. */
+int fg_encode(int dtype, size_t rows, size_t cols, const float *values, void *bytes, void *stream);
+
+/* Matrix::dequantize_row (tensor.rs:247-271): row `row` as f32 into device `out` (cols long). */
+int fg_dequantize_row(const fg_table *table, size_t row, float *out, void *stream);
+
+/* ------------------------------------------------------------------------ activations */
+
+/* quantize_rows (matmul.rs:233-257): `count` device f32 values, whole groups of the weight
+ * format `dtype`, to int8 levels, one scale and one correction (-zero_point * sum) per group. */
+int fg_quantize_rows(const float *x, size_t count, int dtype, int8_t *quants, float *scales,
+                     int32_t *corrections, void *stream);
+
+/* A matmul input (matmul.rs:107-119): f32 rows to quantize inside the product, or rows already
+ * quantized by fg_quantize_rows for the table's format (all device pointers). Exactly one of
+ * `x` and `quants` is set; `scales` and `corrections` go with `quants`. */
+typedef struct {
+    const float *x;
+    const int8_t *quants;
+    const float *scales;
+    const int32_t *corrections;
+} fg_input;
+
+/* ---------------------------------------------------------------------------- products */
+
+/* matmul + Linear::project_quads (matmul.rs:265-317, linear.rs:52-71): for every input row r
+ * and output column c in [col_begin, col_end) (whole quads, within the table's padded rows),
+ * out[r * ld_out + (c - col_begin)] = row r · W[c] (+ bias[c] when `bias` is set), written, or
+ * added with FG_ACCUMULATE. f32 results are bit-identical to the reference's scalar backend. */
+int fg_matmul(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
+              size_t col_end, const float *bias, float *out, size_t ld_out, int flags, void *stream);
+
+/* The int32 group accumulators of the same product (the dots of matmul.rs:671-709, correction
+ * included): dots[(r * (col_end - col_begin) + (c - col_begin)) * groups + g]. An inspection
+ * entry point for parity checks. */
+int fg_matmul_dots(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
+                   size_t col_end, int32_t *dots, void *stream);
+
+/* ------------------------------------------------------------- the Qwen2 decoder step */
+
+/* Transformer::forward with rows = 1 and Prediction::predict (blocks/src/transformer.rs:294-341,
+ * layer.rs:161-344, lm.rs:147-179) for the Qwen2 architecture: RMSNorm, fused QKV with bias,
+ * rotary embeddings by halves, grouped-query causal attention over an f32 KV cache, a SiLU-gated
+ * feed-forward, a tied embedding/head table. Every projection runs through fg_matmul's kernels. */
+typedef struct {
+    size_t hidden, layers, heads, kv_heads, head_dim, ffn, vocab, capacity;
+    float rope_base, eps;
+    int dtype; /* the weight format of every table */
+    int exact; /* 1: reductions in the reference's order (bit-identical); 0: parallel trees */
+} fg_qwen2_shape;
+
+typedef struct {
+    const float *norm1, *norm2; /* device [hidden] */
+    const float *qkv_bias;      /* device [(heads + 2 kv_heads) head_dim] or NULL */
+    const fg_table *qkv, *o, *gate, *up, *down;
+} fg_qwen2_layer;
+
+typedef struct fg_qwen2 fg_qwen2;
+
+/* The model over caller-owned tables, norms and caches (device [layers][kv_heads][capacity]
+ * [head_dim] f32 each). The handle owns its activation buffers only. */
+int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer *layers, const float *final_norm,
+                    const fg_table *table, float *kcache, float *vcache, fg_qwen2 **out);
+/* One token at `position`: embedding, every layer, final norm, logits and the greedy token.
+ * Outputs (device, any may be NULL): hidden [hidden], logits [vocab], next_token [1]. */
+int fg_qwen2_step(fg_qwen2 *model, int token, size_t position, float *hidden, float *logits,
+                  int32_t *next_token, void *stream);
+/* One layer over a device hidden row (the residual stream, in and out), for layer-level checks. */
+int fg_qwen2_layer_forward(fg_qwen2 *model, size_t layer, size_t position, float *hidden, void *stream);
+int fg_qwen2_free(fg_qwen2 *model);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

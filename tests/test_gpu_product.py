@@ -1,0 +1,289 @@
+"""GPU parity of the product path against the CPU oracle: bit-exact bytes, levels, scales,
+corrections, int32 group accumulators and f32 outputs, through the C ABI."""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from gpu_data import activations, encoded_table, synthetic_table
+
+pytestmark = pytest.mark.gpu
+
+PRODUCT_FORMATS = [O.Q7B32, O.Q8B32, O.Q4B32]
+ALL_FORMATS = [O.Q7B32, O.Q8B32, O.Q4B32, O.T2B128]
+
+
+@pytest.fixture(scope="module")
+def fk(gpu):
+    import fusor_kernels
+    return fusor_kernels
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def table(fk, dtype, rows, cols, data):
+    return fk.Table(fk.Tensor(dtype, [rows, cols], data))
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def first_mismatch(a, b):
+    a = np.asarray(a, np.float32).reshape(-1)
+    b = np.asarray(b, np.float32).reshape(-1)
+    bad = np.nonzero(a.view(np.uint32) != b.view(np.uint32))[0]
+    return (int(bad[0]), float(a[bad[0]]), float(b[bad[0]]), len(bad)) if len(bad) else None
+
+
+# ------------------------------------------------------------------------------- tables
+
+@pytest.mark.parametrize("dtype", ALL_FORMATS)
+@pytest.mark.parametrize("rows,cols", [(4, 128), (25, 128), (7, 256), (130, 512)])
+def test_table_upload_keeps_the_reference_bytes(fk, dtype, rows, cols):
+    data = encoded_table(dtype, rows, cols, seed=rows * 7 + dtype)
+    t = table(fk, dtype, rows, cols, data)
+    assert np.array_equal(t.reference_bytes(), data)
+
+
+@pytest.mark.parametrize("dtype", ALL_FORMATS)
+def test_encode_matches_the_oracle(fk, dtype):
+    rng = np.random.default_rng(dtype)
+    rows, cols = 9, 256
+    values = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    values[0, :32] = 0.0                                   # an all-zero group
+    values[1, 5] = np.float32(np.frombuffer(np.uint32(94).tobytes(), np.float32)[0])  # subnormal
+    values[1, 32:64] = 0.0
+    values[1, 40] = np.frombuffer(np.uint32(94).tobytes(), np.float32)[0]
+    values[2, 70] = np.nan
+    values[3, 3] = np.inf
+    values[4, 130] = -np.inf
+    values[5, :128] = np.repeat(np.float32([0.5, -0.5]), 64)  # ties
+    got = fk.Tensor.encode(fk.DType(dtype), [rows, cols], values).bytes()
+    want = O.encode(dtype, rows, cols, values)
+    assert np.array_equal(got, want)
+
+
+def test_encode_rejects_partial_groups(fk):
+    with pytest.raises(fk.FormatError, match=r"a T2b128 tensor of shape \[1, 64\]: a matrix of whole groups of 128 expected"):
+        fk.Tensor.encode(fk.DType.T2b128, [1, 64], np.ones(64, np.float32))
+    with pytest.raises(fk.FormatError, match=r"63 values for a tensor of shape \[2, 32\]"):
+        fk.Tensor.encode(fk.DType.Q7b32, [2, 32], np.ones(63, np.float32))
+
+
+@pytest.mark.parametrize("dtype", ALL_FORMATS)
+def test_dequantize_row_matches_the_oracle(fk, dtype):
+    import torch
+    rows, cols = 11, 256
+    data = encoded_table(dtype, rows, cols, seed=3 + dtype)
+    t = table(fk, dtype, rows, cols, data)
+    out = torch.empty(cols, dtype=torch.float32, device="cuda")
+    for r in range(rows):
+        t.matrix().dequantize_row(r, out)
+        assert same_bits(host(out), O.dequantize_row(dtype, rows, cols, data, r)), r
+    with pytest.raises(fk.ShapeError):
+        t.matrix().dequantize_row(rows, out)
+
+
+# ----------------------------------------------------------------- activation quantization
+
+@pytest.mark.parametrize("dtype", ALL_FORMATS)
+@pytest.mark.parametrize("count", [128, 896, 4864 * 3, 4096 * 16])
+def test_quantize_rows_matches_the_oracle(fk, dtype, count):
+    import torch
+    x = activations(1, count, seed=count + dtype, outliers=0.01).reshape(-1)
+    x[:32] = 0.0
+    x[40] = np.frombuffer(np.uint32(381).tobytes(), np.float32)[0]
+    x[count // 2 + 3] = np.nan
+    if count > 1000:
+        x[900] = np.inf
+    g = O.group(dtype)
+    q = torch.empty(count, dtype=torch.int8, device="cuda")
+    s = torch.empty(count // g, dtype=torch.float32, device="cuda")
+    c = torch.empty(count // g, dtype=torch.int32, device="cuda")
+    import fusor_kernels as fk2
+    fk2.quantize_rows(dev(x), fk2.QuantFormat(dtype), q, s, c)
+    wq, ws, wc = O.quantize_rows(x, dtype)
+    assert np.array_equal(host(q), wq)
+    assert same_bits(host(s), ws)
+    assert np.array_equal(host(c), wc)
+
+
+# ------------------------------------------------------------------------------ products
+
+def gpu_product(fk, t, x, rows, cols=None, fused=True, bias=None, dots=False):
+    import torch
+    m = t.matrix()
+    if cols is None:
+        cols = range(0, (t.rows + 3) // 4 * 4)
+    if fused:
+        inp = fk.Input(f32=dev(x.reshape(-1)))
+    else:
+        inp = fk.QuantizedRows().input(m, dev(x.reshape(-1)))
+    if dots:
+        return host(fk.matmul_dots(m, inp, cols))
+    out = fk.matmul(m, inp, cols, bias=None if bias is None else dev(bias))
+    return host(out)
+
+
+def oracle_product(dtype, rows_w, cols_w, data, x, rows, col_begin=0, col_end=None, bias=None, want_dots=False):
+    q, s, c = O.quantize_rows(x.reshape(-1), dtype)
+    return O.matmul(dtype, rows_w, cols_w, data, q, s, c, rows, col_begin, col_end, bias=bias, want_dots=want_dots)
+
+
+@pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8, 16, 33, 64, 100])
+def test_product_is_bit_exact(fk, dtype, rows):
+    n_rows, cols = 37, 256
+    data = synthetic_table(dtype, n_rows, cols, seed=rows)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=100 + rows, outliers=0.02)
+    want, want_dots = oracle_product(dtype, n_rows, cols, data, x, rows, want_dots=True)
+    got = gpu_product(fk, t, x, rows)
+    assert same_bits(got, want), first_mismatch(got, want)
+    got_dots = gpu_product(fk, t, x, rows, dots=True)
+    assert np.array_equal(got_dots, want_dots)
+
+
+@pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
+@pytest.mark.parametrize("rows", [1, 3, 17])
+def test_prequantized_input_equals_in_kernel_quantization(fk, dtype, rows):
+    n_rows, cols = 64, 512
+    data = synthetic_table(dtype, n_rows, cols, seed=5)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=6)
+    assert same_bits(gpu_product(fk, t, x, rows, fused=True), gpu_product(fk, t, x, rows, fused=False))
+
+
+@pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
+@pytest.mark.parametrize("rows", [1, 6])
+def test_column_ranges_bias_and_residual(fk, dtype, rows):
+    import torch
+    n_rows, cols = 50, 128
+    data = synthetic_table(dtype, n_rows, cols, seed=9)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=10)
+    bias = np.random.default_rng(1).standard_normal(n_rows).astype(np.float32)
+    want = oracle_product(dtype, n_rows, cols, data, x, rows, 8, 40, bias=bias)
+    got = gpu_product(fk, t, x, rows, cols=range(8, 40), bias=bias)
+    assert same_bits(got, want)
+    # the padding quad past row 50: zero codes and scales, no bias (linear.rs:63-68)
+    tail = gpu_product(fk, t, x, rows, cols=range(48, 52), bias=bias)
+    wtail = oracle_product(dtype, n_rows, cols, data, x, rows, 48, 52, bias=bias)
+    assert same_bits(tail, wtail)
+    # project_residual_input: h = fl(h + y) (linear.rs:134-143)
+    h0 = np.random.default_rng(2).standard_normal((rows, n_rows)).astype(np.float32)
+    h = dev(h0)
+    lin = fk.Linear(t, None)
+    inp = fk.QuantizedRows().input(t.matrix(), dev(x.reshape(-1)))
+    fk.project_residual_input(fk.Ctx(0, 1), lin, inp, h)
+    full = oracle_product(dtype, n_rows, cols, data, x, rows)[:, :n_rows]
+    upto = n_rows // 16 * 16
+    want_h = h0.copy()
+    want_h[:, :upto] = (h0[:, :upto] + full[:, :upto]).astype(np.float32)
+    assert same_bits(host(h), want_h)
+    with pytest.raises(fk.ShapeError, match="columns in whole quads"):
+        gpu_product(fk, t, x, rows, cols=range(2, 8))
+    with pytest.raises(fk.ShapeError, match="weights cover the columns"):
+        gpu_product(fk, t, x, rows, cols=range(0, 56))
+
+
+def pseudo_random(n, seed):
+    """matmul.rs:772-780"""
+    state = seed & 0xFFFFFFFF
+    out = np.empty(n, np.float32)
+    for i in range(n):
+        state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+        out[i] = np.float32(state >> 8) / np.float32(1 << 24) * np.float32(2.0) - np.float32(1.0)
+    return out
+
+
+@pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
+def test_every_format_matches_the_dequantized_product(fk, dtype):
+    """matmul.rs:809-843 through the GPU: 25 x 128, rows 1/3/8/11; bit-exact against the oracle
+    and within the reference's own f64 tolerance."""
+    outputs, width = 25, 128
+    data = O.encode(dtype, outputs, width, pseudo_random(outputs * width, 1))
+    t = table(fk, dtype, outputs, width, data)
+    w = O.dequantize(dtype, outputs, width, data).astype(np.float64)
+    for rows in (1, 3, 8, 11):
+        x = pseudo_random(rows * width, 7 + rows).reshape(rows, width)
+        got = gpu_product(fk, t, x, rows)
+        assert same_bits(got, oracle_product(dtype, outputs, width, data, x, rows))
+        for r in range(rows):
+            qx = np.empty(width)
+            for k in range(0, width, 32):
+                blk = x[r, k:k + 32]
+                sc = np.max(np.abs(blk)) / np.float32(127.0)
+                qx[k:k + 32] = (np.rint(blk / sc) * sc).astype(np.float32)
+            want = w @ qx
+            assert np.all(np.abs(got[r, :outputs] - want) < 1e-4 * (1 + np.abs(want)))
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32])
+def test_single_matvec_shape_bit_exact(fk, dtype):
+    """4864 x 896, one row ~N(0,1), seed 0: every output and accumulator bit-exact."""
+    rows_w, cols = 4864, 896
+    data = synthetic_table(dtype, rows_w, cols, seed=0)
+    t = table(fk, dtype, rows_w, cols, data)
+    x = activations(1, cols, seed=0)
+    want, want_dots = oracle_product(dtype, rows_w, cols, data, x, 1, want_dots=True)
+    assert same_bits(gpu_product(fk, t, x, 1), want)
+    assert same_bits(gpu_product(fk, t, x, 1, fused=False), want)
+    assert np.array_equal(gpu_product(fk, t, x, 1, dots=True), want_dots)
+
+
+@pytest.mark.parametrize("shape", [(512, 896, 9728), (512, 4864, 896), (4096, 1152, 3456), (4096, 4608, 1152)])
+def test_batched_shapes_bit_exact_on_sampled_rows(fk, shape):
+    """Full-size GEMMs; the oracle checks a sample of rows over every column (rows are
+    independent)."""
+    rows, k, n = shape
+    data = synthetic_table(O.Q8B32, n, k, seed=rows + k)
+    t = table(fk, O.Q8B32, n, k, data)
+    x = (activations(rows, k, seed=k, outliers=0.01) * np.float32(np.sqrt(2.0))).astype(np.float32)
+    got = gpu_product(fk, t, x, rows)
+    sample = [0, 1, 31, 32, 63, rows // 2 + 5, rows - 1]
+    want = oracle_product(O.Q8B32, n, k, data, x[sample], len(sample))
+    assert same_bits(got[sample], want), first_mismatch(got[sample], want)
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_int4_shape_bit_exact(fk, rows):
+    n, k = 14336, 4096
+    data = synthetic_table(O.Q4B32, n, k, seed=4)
+    t = table(fk, O.Q4B32, n, k, data)
+    x = activations(rows, k, seed=44)
+    got = gpu_product(fk, t, x, rows)
+    sample = list(range(rows)) if rows <= 2 else [0, 5, 15]
+    want = oracle_product(O.Q4B32, n, k, data, x[sample], len(sample))
+    assert same_bits(got[sample], want), first_mismatch(got[sample], want)
+
+
+def test_batched_rows_equal_row_by_row_products(fk):
+    """A size-independent property: the matrix-core path and the matrix-vector path are the same
+    function of each row."""
+    n, k, rows = 1152, 896, 24
+    data = synthetic_table(O.Q7B32, n, k, seed=8)
+    t = table(fk, O.Q7B32, n, k, data)
+    x = activations(rows, k, seed=8)
+    batched = gpu_product(fk, t, x, rows)
+    for r in range(0, rows, 5):
+        assert same_bits(batched[r:r + 1], gpu_product(fk, t, x[r:r + 1], 1))
+
+
+def test_zero_rows_and_empty_ranges(fk):
+    data = synthetic_table(O.Q7B32, 8, 64, seed=1)
+    t = table(fk, O.Q7B32, 8, 64, data)
+    x = activations(2, 64, seed=1)
+    assert gpu_product(fk, t, x, 2, cols=range(4, 4)).shape == (2, 0)

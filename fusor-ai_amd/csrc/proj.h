@@ -1,0 +1,98 @@
+// The projection kernel's parameter block, modes and LDS layout, shared by the generic product
+// and the decoder.
+#pragma once
+
+#include "common.h"
+
+namespace fg {
+
+// Input of a projection: rows already quantized, f32 rows quantized in-kernel, or one f32 row
+// RMS-normalized then quantized in-kernel (rms_norm, ops.rs:7-16).
+constexpr int IN_PREQ = 0, IN_F32 = 1, IN_NORM = 2;
+// Output: store (bias / residual / greedy candidates), the int32 group accumulators, the QKV
+// epilogue, the gated feed-forward epilogue.
+constexpr int OUT_STORE = 0, OUT_DOTS = 1, OUT_QKV = 2, OUT_SWIGLU = 3;
+
+struct ProjParams {
+    const int8_t *codes, *codes2;      // device table(s); codes2 is the SwiGLU up table
+    const float *wscales, *wscales2;
+    int B, G, K, n_rows;
+    int quad_begin, quad_end, qpw;
+    // input
+    const float *x;
+    const int8_t *q;
+    const float *as;
+    const int32_t *corr;
+    int zp;
+    const float *norm_w;
+    float eps;
+    // store
+    const float *bias;
+    float *out;
+    long ld_out;
+    int col_begin, accumulate;
+    int32_t *dots;
+    int dots_cols;
+    float *pval;  // greedy candidates per workgroup, or null
+    int32_t *pidx;
+    // QKV epilogue
+    float *qkv_out;
+    const float *rope;  // cos[half] then sin[half] of the position
+    int heads, kv_heads, D;
+    float *kcache, *vcache;
+    size_t layer_base;
+    int capacity, position;
+    // SwiGLU epilogue: the down projection's quantized input
+    int8_t *q_out;
+    float *s_out;
+    int32_t *c_out;
+    int zp_out;
+};
+
+// Byte offsets of the LDS regions (every region 16-byte aligned).
+struct ProjLayout {
+    int off_s, off_c, off_red, off_y, off_terms, off_n, total;
+};
+
+__host__ __device__ inline int align16(int b) { return (b + 15) & ~15; }
+
+__host__ __device__ inline ProjLayout proj_layout(int R, int K, int G, int NW, int in, int out)
+{
+    const int NT = out == OUT_SWIGLU ? 2 : 1;
+    const int ny = out == OUT_SWIGLU ? 3 : 1;
+    ProjLayout l;
+    l.off_s = align16(R * K);
+    l.off_c = l.off_s + align16(R * G * 4);
+    l.off_red = l.off_c + align16(R * G * 4);
+    l.off_y = l.off_red + 16 * 4;
+    l.off_terms = l.off_y + align16(ny * R * NW * 4);
+    l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * G * NW * 4));
+    l.total = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);
+    return l;
+}
+
+// ops::exp (ops.rs:97-131): clamp, n = round(x·log2 e), r = x − n·ln2_hi − n·ln2_lo, Cephes
+// polynomial in Horner order, times 2^n through the exponent bits. No fused multiply-add.
+__device__ __forceinline__ float ref_exp(float x)
+{
+    x = x < -87.0f ? -87.0f : (x > 88.0f ? 88.0f : x);
+    const float exponent = __builtin_rintf(x * 1.44269504088896340736f);
+    const float remainder = x - exponent * 0.6933594f - exponent * -2.1219444e-4f;
+    float poly = 1.9875691e-4f;
+    poly = poly * remainder + 1.3981999e-3f;
+    poly = poly * remainder + 8.333452e-3f;
+    poly = poly * remainder + 4.1665796e-2f;
+    poly = poly * remainder + 0.16666666f;
+    poly = poly * remainder + 0.5f;
+    poly = poly * remainder * remainder + remainder + 1.0f;
+    const int bits = (int(exponent) + 127) << 23;
+    return poly * __int_as_float(bits);
+}
+
+// ops::silu (ops.rs:272-274)
+__device__ __forceinline__ float ref_silu(float x) { return x / (1.0f + ref_exp(-x)); }
+
+size_t proj_smem(const ProjParams &p, int rows, int in, int out);
+int launch_proj(const ProjParams &p, int dtype, int in, int out, bool exact, hipStream_t s);
+
+}  // namespace fg

@@ -29,7 +29,6 @@ namespace fg {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBatch = 8;
 
 __device__ __forceinline__ int dot16(int4 w, int4 a) { return dot4(w.w, a.w, dot4(w.z, a.z, dot4(w.y, a.y, dot4(w.x, a.x, 0)))); }
 
@@ -256,7 +255,7 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
 }
 
 // FMT: 8 for signed 8-bit levels (Q7b32 folded, Q8b32), 4 for offset nibbles (Q4b32).
-template <int FMT, int R, int IN, int OUT, bool EXACT>
+template <int FMT, int R, int IN, int OUT, bool EXACT, int kBatch>
 __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -349,6 +348,13 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     float sa[kBatch], sb[kBatch];
     StageRegs g;
     stage_issue<R, IN>(p, g);
+    // the residual row this workgroup adds to, read early (linear.rs:139-142)
+    float resid = 0.0f;
+    if (OUT == OUT_STORE && p.accumulate) {
+        const int r = int(threadIdx.x) / NW, nl = int(threadIdx.x) - r * NW;
+        const bool mine = r < R && nl < nq * 4;
+        resid = p.out[mine ? r * p.ld_out + (qa * 4 + nl - p.col_begin) : 0];
+    }
     if (batches > 0) load(0, wa, sa);
     stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
     __syncthreads();
@@ -374,7 +380,9 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         if (OUT != OUT_SWIGLU && p.bias && n < p.n_rows) s = s + p.bias[n];
         if (OUT == OUT_STORE) {
             float *o = p.out + r * p.ld_out + (n - p.col_begin);
-            *o = p.accumulate ? *o + s : s;
+            float prior = resid;
+            if (p.accumulate && i >= kThreads) prior = *o;  // rows past the prefetched ones
+            *o = p.accumulate ? prior + s : s;
         }
         ybuf[i] = s;
     }
@@ -457,10 +465,10 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     }
 }
 
-template <int FMT, int R, int IN, int OUT, bool EXACT>
+template <int FMT, int R, int IN, int OUT, bool EXACT, int NB = 8>
 int launch_one(const ProjParams &p, size_t smem, unsigned grid, hipStream_t s)
 {
-    auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT>;
+    auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT, NB>;
     if (smem > 64 * 1024) {
         static bool raised = false;
         if (!raised) {
@@ -494,10 +502,12 @@ int dispatch_rows(const ProjParams &p, int rows, int in, bool dots, size_t smem,
     }
 }
 
-template <int FMT, int IN, int OUT>
+// The decoder's launches: 16 chunks per wave in flight where workgroups are few (one per head or
+// per 32 outputs), 8 where they are many.
+template <int FMT, int IN, int OUT, int NB>
 int dispatch_exact(const ProjParams &p, bool exact, size_t smem, unsigned grid, hipStream_t s)
 {
-    return exact ? launch_one<FMT, 1, IN, OUT, true>(p, smem, grid, s) : launch_one<FMT, 1, IN, OUT, false>(p, smem, grid, s);
+    return exact ? launch_one<FMT, 1, IN, OUT, true, NB>(p, smem, grid, s) : launch_one<FMT, 1, IN, OUT, false, NB>(p, smem, grid, s);
 }
 
 }  // namespace
@@ -518,15 +528,17 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     const bool q4 = dtype == FG_Q4B32;
     switch (out) {
     case OUT_QKV:
-        return q4 ? dispatch_exact<4, IN_NORM, OUT_QKV>(p, exact, smem, grid, s) : dispatch_exact<8, IN_NORM, OUT_QKV>(p, exact, smem, grid, s);
+        return q4 ? dispatch_exact<4, IN_NORM, OUT_QKV, 16>(p, exact, smem, grid, s)
+                  : dispatch_exact<8, IN_NORM, OUT_QKV, 16>(p, exact, smem, grid, s);
     case OUT_SWIGLU:
-        return q4 ? dispatch_exact<4, IN_NORM, OUT_SWIGLU>(p, exact, smem, grid, s)
-                  : dispatch_exact<8, IN_NORM, OUT_SWIGLU>(p, exact, smem, grid, s);
+        return q4 ? dispatch_exact<4, IN_NORM, OUT_SWIGLU, 16>(p, exact, smem, grid, s)
+                  : dispatch_exact<8, IN_NORM, OUT_SWIGLU, 16>(p, exact, smem, grid, s);
     default:
         if (in == IN_NORM)
-            return q4 ? dispatch_exact<4, IN_NORM, OUT_STORE>(p, exact, smem, grid, s)
-                      : dispatch_exact<8, IN_NORM, OUT_STORE>(p, exact, smem, grid, s);
-        return q4 ? launch_one<4, 1, IN_PREQ, OUT_STORE, false>(p, smem, grid, s) : launch_one<8, 1, IN_PREQ, OUT_STORE, false>(p, smem, grid, s);
+            return q4 ? dispatch_exact<4, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s)
+                      : dispatch_exact<8, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s);
+        return q4 ? launch_one<4, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s)
+                  : launch_one<8, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s);
     }
 }
 

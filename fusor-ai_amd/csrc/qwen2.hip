@@ -2,10 +2,11 @@
 // Prediction::predict (blocks/src/transformer.rs:185-341, layer.rs:161-344,
 // layer/input.rs:22-66, lm.rs:97-179), every projection through the projection kernel.
 //
-// Five launches per layer, each projection with its neighbours fused in:
+// Six launches per layer, each projection with its neighbours fused in:
 //   1. RMSNorm + quantize -> QKV product + bias -> RoPE on query/key heads, keys and values kept
-//   2. attention of every query head over the cache (scores, softmax, weighted values), output
-//      quantized for the output projection
+//   2. attention of every query head over the cache in two launches: the scores by key blocks,
+//      then softmax and weighted values by head and 32 value dimensions, quantized for the output
+//      projection
 //   3. output projection added to the residual row
 //   4. RMSNorm + quantize -> gate and up products -> silu(gate)·up quantized for down
 //   5. down projection added to the residual row
@@ -27,18 +28,85 @@ namespace fg {
 namespace {
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnRegs = 32;  // float4 per thread for one staged chunk of keys or values
+constexpr int kScoreKeys = 32;   // keys per workgroup of the scores
+constexpr int kWeighKeys = 256;  // keys per staged chunk of values
+constexpr int kWeighDims = 32;   // value dimensions per workgroup (one quantization group)
 
 struct AttnParams {
     const float *qkv;  // rotated query heads first
     const float *kcache, *vcache;
     size_t layer_base;
-    int heads, kv_heads, D, capacity, keys, chunk;
+    int heads, kv_heads, D, capacity, keys;
+    float *scores;  // [heads][capacity]
     int zp;
     int8_t *q;
     float *scales;
     int32_t *corr;
 };
+
+// Scores of every query head of one KV head against kScoreKeys keys (ops.rs:310-326):
+// dot_f32(q, k_j) in index order, times 1/√D. Grid: (kv_heads, key blocks).
+__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnParams a)
+{
+    extern __shared__ __align__(16) float ash[];
+    const int D = a.D, S = D + 1;
+    const int group = a.heads / a.kv_heads;
+    const int kv = blockIdx.x, j0 = int(blockIdx.y) * kScoreKeys;
+    const int n = min(kScoreKeys, a.keys - j0);
+    float *krows = ash;                      // [kScoreKeys][D + 1]
+    float *query = krows + kScoreKeys * S;   // [group][D]
+    const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
+    // all loads first (branch-free: past-the-end rows re-read row j0)
+    const int per_row = D / 4;
+    const int nk4 = kScoreKeys * per_row, nq = group * D;
+    float4 kr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int e = int(threadIdx.x) + r * kAttnThreads;
+        const int row = e / per_row, c4 = e - row * per_row;
+        const int rr = (e < nk4 && row < n) ? row : 0;
+        kr[r] = *reinterpret_cast<const float4 *>(kbase + size_t((j0 + rr) % a.capacity) * D + c4 * 4);
+    }
+    float qv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int e = int(threadIdx.x) + r * kAttnThreads;
+        qv[r] = a.qkv[size_t(kv * group) * D + min(e, nq - 1)];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int e = int(threadIdx.x) + r * kAttnThreads;
+        const int row = e / per_row, c4 = e - row * per_row;
+        if (e < nk4) {
+            float *dst = krows + row * S + c4 * 4;
+            dst[0] = kr[r].x;
+            dst[1] = kr[r].y;
+            dst[2] = kr[r].z;
+            dst[3] = kr[r].w;
+        }
+        if (e < nq) query[e] = qv[r];
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(float(D));
+    for (int t = threadIdx.x; t < group * kScoreKeys; t += kAttnThreads) {
+        const int h = t / kScoreKeys, j = t - h * kScoreKeys;
+        if (j >= n) continue;
+        const float *k = krows + j * S;
+        const float *q = query + h * D;
+        float s = -0.0f;  // dot_f32 in index order (arch/scalar.rs:340-342)
+        for (int d = 0; d < D; d += 16) {
+            float x[16], y[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                x[e] = q[d + e];
+                y[e] = k[d + e];
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) s = s + x[e] * y[e];
+        }
+        a.scores[size_t(kv * group + h) * a.capacity + j0 + j] = s * scale;
+    }
+}
 
 __device__ float attn_block_max(float v, float *red)
 {
@@ -58,171 +126,130 @@ __device__ float attn_block_sum(float v, float *red)
     return ((red[4] + red[5]) + red[6]) + red[7];
 }
 
-// Rows [j0, j0 + n) of one head of the cache (positions mod capacity) into registers, float4 by
-// float4; then into LDS rows of D + 1 floats (conflict-free column reads).
-__device__ __forceinline__ void fetch_rows(const float *base, int capacity, int D, int j0, int n, float4 *regs)
+// kWeighKeys keys x kWeighDims dims of one KV head's values into registers (8 float4 per thread),
+// branch-free.
+__device__ __forceinline__ void fetch_values(const float *vbase, int capacity, int D, int d0, int j0, int n, float4 *r)
 {
-    const int per_row = D / 4;
 #pragma unroll
-    for (int r = 0; r < kAttnRegs; r++) {
-        const int e = int(threadIdx.x) + r * kAttnThreads;  // float4 index within the chunk
-        const int row = e / per_row, c4 = e - row * per_row;
-        // branch-free (rows past n re-read row j0), so that every load issues before any wait
+    for (int k = 0; k < 8; k++) {
+        const int e = int(threadIdx.x) + k * kAttnThreads;  // float4 index: row e / 8, column (e % 8) * 4
+        const int row = e >> 3, c4 = e & 7;
         const int rr = row < n ? row : 0;
-        regs[r] = *reinterpret_cast<const float4 *>(base + size_t((j0 + rr) % capacity) * D + c4 * 4);
+        r[k] = *reinterpret_cast<const float4 *>(vbase + size_t((j0 + rr) % capacity) * D + d0 + c4 * 4);
     }
 }
 
-__device__ __forceinline__ void stash_rows(const float4 *regs, int D, int n, float *lds)
-{
-    const int per_row = D / 4, S = D + 1;
-#pragma unroll
-    for (int r = 0; r < kAttnRegs; r++) {
-        const int e = int(threadIdx.x) + r * kAttnThreads;
-        const int row = e / per_row, c4 = e - row * per_row;
-        if (row < n) {
-            float *dst = lds + row * S + c4 * 4;
-            dst[0] = regs[r].x;
-            dst[1] = regs[r].y;
-            dst[2] = regs[r].z;
-            dst[3] = regs[r].w;
-        }
-    }
-}
-
-// ops::attend for one query head over positions 0..keys-1 (ops.rs:310-342 under Mask::Causal,
-// transformer.rs:185-219): scores = dot_f32(q, k_j)·(1/√D), softmax with ops::exp, the weighted
-// sum of values; then the head's output quantized for the output projection.
+// Softmax of one head's scores (ops.rs:301-306: maximum, ops::exp, the total, the division) and
+// the weighted sum of kWeighDims value dimensions (ops.rs:329-342), then those outputs quantized
+// (one group) for the output projection. Grid: (heads, D / kWeighDims).
 template <bool EXACT>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnParams a)
+__global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
 {
     extern __shared__ __align__(16) float ash[];
-    const int D = a.D, S = D + 1, keys = a.keys, CH = a.chunk;
-    float *rows = ash;                 // [CH][D + 1]
-    float *score = rows + CH * S;      // [keys]
-    float *query = score + keys;       // [D]
-    float *parts = query + D;          // [4][D]
-    float *out = parts + 4 * D;        // [D]
-    float *red = out + D;              // [16]
-    const int head = blockIdx.x;
+    constexpr int S = kWeighDims + 1;
+    const int D = a.D, keys = a.keys;
+    const int head = blockIdx.x, d0 = int(blockIdx.y) * kWeighDims;
     const int kv = head / (a.heads / a.kv_heads);
-    const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
+    float *vrows = ash;                    // [kWeighKeys][kWeighDims + 1]
+    float *w = vrows + kWeighKeys * S;     // [keys]
+    float *parts = w + a.capacity;         // [8][kWeighDims]
+    float *red = parts + 8 * kWeighDims;   // [16]
     const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D;
-    float4 regs[kAttnRegs];
-
-    fetch_rows(kbase, a.capacity, D, 0, min(CH, keys), regs);
-    for (int i = threadIdx.x; i < D; i += kAttnThreads) query[i] = a.qkv[head * D + i];
-    const float scale = 1.0f / sqrtf(float(D));
+    const float *sc = a.scores + size_t(head) * a.capacity;
+    float4 vr[8];
+    fetch_values(vbase, a.capacity, D, d0, 0, min(kWeighKeys, keys), vr);
     float local_max = -INFINITY;
-    for (int j0 = 0; j0 < keys; j0 += CH) {
-        const int n = min(CH, keys - j0);
-        __syncthreads();
-        stash_rows(regs, D, n, rows);
-        __syncthreads();
-        if (j0 + CH < keys) fetch_rows(kbase, a.capacity, D, j0 + CH, min(CH, keys - j0 - CH), regs);
-        for (int j = threadIdx.x; j < n; j += kAttnThreads) {
-            const float *k = rows + j * S;
-            float s = -0.0f;  // dot_f32 in index order
-            for (int d = 0; d < D; d += 16) {
-                float qv[16], kv[16];
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    qv[e] = query[d + e];
-                    kv[e] = k[d + e];
-                }
-#pragma unroll
-                for (int e = 0; e < 16; e++) s = s + qv[e] * kv[e];
-            }
-            s = s * scale;
-            score[j0 + j] = s;
-            local_max = fmaxf(local_max, s);
-        }
+    for (int j = threadIdx.x; j < keys; j += kAttnThreads) {
+        const float s = sc[j];
+        w[j] = s;
+        local_max = fmaxf(local_max, s);
     }
-    // the first chunk of values is on its way while the softmax runs
-    fetch_rows(vbase, a.capacity, D, 0, min(CH, keys), regs);
     const float peak = attn_block_max(local_max, red);
-    for (int j = threadIdx.x; j < keys; j += kAttnThreads) score[j] = ref_exp(score[j] - peak);
+    for (int j = threadIdx.x; j < keys; j += kAttnThreads) w[j] = ref_exp(w[j] - peak);
     __syncthreads();
     float total;
     if (EXACT) {
         if (threadIdx.x == 0) {
-            float t = -0.0f;
+            float t = -0.0f;  // the exponentials summed in index order
             int j = 0;
             for (; j + 16 <= keys; j += 16) {
                 float v[16];
 #pragma unroll
-                for (int e = 0; e < 16; e++) v[e] = score[j + e];
+                for (int e = 0; e < 16; e++) v[e] = w[j + e];
 #pragma unroll
                 for (int e = 0; e < 16; e++) t = t + v[e];
             }
-            for (; j < keys; j++) t = t + score[j];
+            for (; j < keys; j++) t = t + w[j];
             red[8] = t;
         }
         __syncthreads();
         total = red[8];
     } else {
         float p = 0.0f;
-        for (int j = threadIdx.x; j < keys; j += kAttnThreads) p = p + score[j];
+        for (int j = threadIdx.x; j < keys; j += kAttnThreads) p = p + w[j];
         total = attn_block_sum(p, red);
     }
-    for (int j = threadIdx.x; j < keys; j += kAttnThreads) score[j] = score[j] / total;
-    // weigh (ops.rs:329-342): out[i] = Σ_j w_j·v_j[i], from +0; exact: index order per output
-    const int slices = EXACT ? 1 : min(4, kAttnThreads / D);
-    const int slice = int(threadIdx.x) / D, i = int(threadIdx.x) - slice * D;
+    for (int j = threadIdx.x; j < keys; j += kAttnThreads) w[j] = w[j] / total;
+    // weigh: out[i] = Σ_j w_j·v_j[i] from +0; exact: index order per output
+    const int slices = EXACT ? 1 : 8;
+    const int slice = int(threadIdx.x) / kWeighDims, i = int(threadIdx.x) - slice * kWeighDims;
     float o = 0.0f;
-    for (int j0 = 0; j0 < keys; j0 += CH) {
-        const int n = min(CH, keys - j0);
+    for (int j0 = 0; j0 < keys; j0 += kWeighKeys) {
+        const int n = min(kWeighKeys, keys - j0);
         __syncthreads();
-        stash_rows(regs, D, n, rows);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int e = int(threadIdx.x) + k * kAttnThreads;
+            const int row = e >> 3, c4 = e & 7;
+            if (row < n) {
+                float *dst = vrows + row * S + c4 * 4;
+                dst[0] = vr[k].x;
+                dst[1] = vr[k].y;
+                dst[2] = vr[k].z;
+                dst[3] = vr[k].w;
+            }
+        }
         __syncthreads();
-        if (j0 + CH < keys) fetch_rows(vbase, a.capacity, D, j0 + CH, min(CH, keys - j0 - CH), regs);
+        if (j0 + kWeighKeys < keys) fetch_values(vbase, a.capacity, D, d0, j0 + kWeighKeys, min(kWeighKeys, keys - j0 - kWeighKeys), vr);
         if (slice < slices) {
             int j = slice;
             for (; j + 16 * slices <= n; j += 16 * slices) {
-                float w[16], v[16];
+                float ww[16], vv[16];
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    w[e] = score[j0 + j + e * slices];
-                    v[e] = rows[(j + e * slices) * S + i];
+                    ww[e] = w[j0 + j + e * slices];
+                    vv[e] = vrows[(j + e * slices) * S + i];
                 }
 #pragma unroll
-                for (int e = 0; e < 16; e++) o = o + w[e] * v[e];
+                for (int e = 0; e < 16; e++) o = o + ww[e] * vv[e];
             }
-            for (; j < n; j += slices) o = o + score[j0 + j] * rows[j * S + i];
+            for (; j < n; j += slices) o = o + w[j0 + j] * vrows[j * S + i];
         }
     }
-    if (slice < slices) parts[slice * D + i] = o;
+    if (slice < slices) parts[slice * kWeighDims + i] = o;
     __syncthreads();
-    for (int k = threadIdx.x; k < D; k += kAttnThreads) {
-        float v = parts[k];
-        for (int s2 = 1; s2 < slices; s2++) v = v + parts[s2 * D + k];
-        out[k] = v;
-    }
-    __syncthreads();
-    // quantize the head's D outputs (D / 32 groups), 8 lanes per group
-    const int groups = D / 32;
-    const int sub = threadIdx.x & 7, g = threadIdx.x >> 3;
-    const bool active = g < groups;
-    float x0 = 0, x1 = 0, x2 = 0, x3 = 0;
-    if (active) {
-        x0 = out[g * 32 + sub * 4];
-        x1 = out[g * 32 + sub * 4 + 1];
-        x2 = out[g * 32 + sub * 4 + 2];
-        x3 = out[g * 32 + sub * 4 + 3];
-    }
-    float amax = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-    amax = fmaxf(0.0f, amax);
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-    const float d = group_scale(amax, 127.0f);
-    const int l0 = quantize_level(x0, d), l1 = quantize_level(x1, d), l2 = quantize_level(x2, d), l3 = quantize_level(x3, d);
-    int sum = l0 + l1 + l2 + l3;
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
-    if (active) {
-        const int G = head * groups + g;
+    // the slices added in order, then the group of kWeighDims outputs quantized (8 lanes)
+    const int sub = threadIdx.x & 7;
+    if (threadIdx.x < 8) {
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float v = parts[sub * 4 + e];
+            for (int s2 = 1; s2 < slices; s2++) v = v + parts[s2 * kWeighDims + sub * 4 + e];
+            x[e] = v;
+        }
+        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        amax = fmaxf(0.0f, amax);
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        const float d = group_scale(amax, 127.0f);
+        const int l0 = quantize_level(x[0], d), l1 = quantize_level(x[1], d), l2 = quantize_level(x[2], d), l3 = quantize_level(x[3], d);
+        int sum = l0 + l1 + l2 + l3;
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        sum += __shfl_xor(sum, 4, 64);
+        const int G = (head * D + d0) / 32;
         reinterpret_cast<int *>(a.q)[G * 8 + sub] = pack4(l0, l1, l2, l3);
         if (sub == 0) {
             a.scales[G] = d;
@@ -292,8 +319,8 @@ struct fg_qwen2 {
     float *pval;
     int32_t *pidx;
     int head_groups;  // workgroups of the head product (greedy candidates)
-    int attn_chunk;
-    size_t attn_smem;
+    float *scores;     // [heads][capacity]
+    size_t score_smem, weigh_smem;
     int zp;
 };
 
@@ -384,13 +411,17 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     a.D = int(sh.head_dim);
     a.capacity = int(sh.capacity);
     a.keys = int(position) + 1;
-    a.chunk = m->attn_chunk;
+    a.scores = m->scores;
     a.zp = m->zp;
     a.q = m->xq;
     a.scales = m->xs;
     a.corr = m->xc;
-    if (sh.exact) attention_kernel<true><<<unsigned(sh.heads), kAttnThreads, m->attn_smem, st>>>(a);
-    else attention_kernel<false><<<unsigned(sh.heads), kAttnThreads, m->attn_smem, st>>>(a);
+    const dim3 sgrid(unsigned(sh.kv_heads), unsigned((a.keys + kScoreKeys - 1) / kScoreKeys));
+    attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
+    FG_HIP(hipGetLastError());
+    const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims));
+    if (sh.exact) attn_weigh_kernel<true><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
+    else attn_weigh_kernel<false><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
     FG_HIP(hipGetLastError());
     return FG_OK;
 }
@@ -461,14 +492,14 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
     m->vcache = vcache;
     m->zp = zero_point_of(sh.dtype);
     m->head_groups = int((table->quads + 63) / 64);
-    // attention: chunks of keys staged in LDS, kAttnRegs float4 per thread
+    // attention LDS: a block of keys and the group's queries; a chunk of values and the weights
     const int D = int(sh.head_dim);
-    m->attn_chunk = kAttnRegs * kAttnThreads * 4 / D;
-    const size_t keys = sh.capacity;
-    m->attn_smem = (size_t(m->attn_chunk) * (D + 1) + keys + D + 4 * D + D + 16) * 4;
-    if (m->attn_smem > 160 * 1024) {
+    const int group = int(sh.heads / sh.kv_heads);
+    m->score_smem = size_t(kScoreKeys * (D + 1) + group * D) * 4;
+    m->weigh_smem = size_t(kWeighKeys * (kWeighDims + 1) + sh.capacity + 8 * kWeighDims + 16) * 4;
+    if (group * D > 4 * kAttnThreads || m->score_smem > 64 * 1024 || m->weigh_smem > 64 * 1024) {
         delete m;
-        return set_error(FG_ERR_SHAPE, "fg_qwen2_create: the attention does not fit in LDS");
+        return set_error(FG_ERR_SHAPE, "fg_qwen2_create: the attention does not fit (heads per KV head x head_dim <= 1024, capacity)");
     }
     const size_t widest = std::max(sh.hidden, std::max(width, sh.ffn));
     const size_t padded_vocab = table->quads * 4;
@@ -485,6 +516,7 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
         {reinterpret_cast<void **>(&m->xc), widest / 32 * 4},
         {reinterpret_cast<void **>(&m->pval), size_t(m->head_groups) * 4},
         {reinterpret_cast<void **>(&m->pidx), size_t(m->head_groups) * 4},
+        {reinterpret_cast<void **>(&m->scores), sh.heads * sh.capacity * 4},
     };
     for (auto &a : allocs) {
         hipError_t e = hipMalloc(a.ptr, a.bytes);
@@ -495,13 +527,6 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
         }
     }
     hipError_t e = hipSuccess;
-    if (m->attn_smem > 64 * 1024) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(attention_kernel<true>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void *>(attention_kernel<false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    }
     // Rotary angles per position (blocks/src/rotary.rs angles; ops.rs:70-74), on the host in f32
     // with the C library's powf/cosf/sinf, as the reference computes them.
     const size_t half = sh.head_dim / 2;
@@ -564,7 +589,7 @@ extern "C" int fg_qwen2_step(fg_qwen2 *m, int token, size_t position, float *hid
 extern "C" int fg_qwen2_free(fg_qwen2 *m)
 {
     if (!m) return FG_OK;
-    void *ptrs[] = {m->hidden, m->qkv, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx};
+    void *ptrs[] = {m->hidden, m->qkv, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete m;

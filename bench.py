@@ -299,6 +299,9 @@ def main():
     ap.add_argument("--exact", action="store_true", help="time the exact-order decoder as the headline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="skip the extra workloads")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run 5 device-to-device copies of this many MiB (the known-size kernel that scales "
+                         "the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus 1 only)", file=sys.stderr)
@@ -361,6 +364,13 @@ def main():
         "cpu_baseline": cpu,
     }
     line.update(other)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_calibration_bytes"] = src.numel() * 4
     print(json.dumps(line), flush=True)
 
 

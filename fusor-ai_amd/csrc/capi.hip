@@ -126,7 +126,6 @@ static int check_product(const fg_table *t, const fg_input *in, size_t rows, siz
     if (in->quants && (reinterpret_cast<uintptr_t>(in->quants) & 15))
         return set_error(FG_ERR_ARG, std::string(who) + ": quants must be 16-byte aligned");
     if (rows > (size_t(1) << 24)) return set_error(FG_ERR_SHAPE, "too many rows");
-    if (t->dtype == FG_T2B128) return set_error(FG_ERR_FORMAT, "T2b128 products are not built on the GPU");
     return FG_OK;
 }
 

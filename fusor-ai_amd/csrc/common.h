@@ -128,5 +128,6 @@ struct ProductArgs {
 };
 int launch_matvec(const ProductArgs &a, hipStream_t s);
 int launch_gemm(const ProductArgs &a, hipStream_t s);
+int launch_t2(const ProductArgs &a, hipStream_t s);
 int launch_product(const ProductArgs &a, hipStream_t s);
 }  // namespace fg

@@ -146,12 +146,86 @@ int launch_tiles(const GemmParams &p, bool dots, hipStream_t s)
     return FG_OK;
 }
 
+// T2b128 (ternary levels, one scale per 128 inputs: matmul.rs:461-469, quant.rs:168-177): one
+// thread per (row, output), the groups in order, each group's four blocks summed as integers
+// before the scaling (matmul.rs:671-709). Device row-block of 8 bytes: byte i holds the offset
+// codes of inputs i, i + 8, i + 16, i + 24 in its bit pairs. Not tuned: no workload uses it.
+__global__ __launch_bounds__(256) void t2_product_kernel(const uint8_t *__restrict__ codes, const float *__restrict__ wscales,
+                                                         int B, int G, int K, int n_rows, const int8_t *__restrict__ q,
+                                                         const float *__restrict__ as, const int32_t *__restrict__ corr,
+                                                         int rows, int col_begin, int ncols, const float *__restrict__ bias,
+                                                         float *out, long ld_out, int accumulate, int32_t *dots)
+{
+    const long id = long(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= long(rows) * ncols) return;
+    const int r = int(id / ncols), c = int(id % ncols);
+    const int n = col_begin + c, quad = n >> 2, L = n & 3;
+    const int8_t *qa = q + size_t(r) * K;
+    float s = 0.0f;
+    for (int g = 0; g < G; g++) {
+        int D = corr[size_t(r) * G + g];
+        for (int b = 4 * g; b < 4 * g + 4; b++) {
+            const uint8_t *rb = codes + (size_t(quad) * B + b) * 32 + L * 8;
+            const int lo = *reinterpret_cast<const int *>(rb), hi = *reinterpret_cast<const int *>(rb + 4);
+            const int *ad = reinterpret_cast<const int *>(qa + b * 32);
+            for (int t = 0; t < 4; t++) {
+                D = dot4((lo >> (2 * t)) & 0x03030303, ad[2 * t], D);
+                D = dot4((hi >> (2 * t)) & 0x03030303, ad[2 * t + 1], D);
+            }
+        }
+        if (dots) {
+            dots[(size_t(r) * ncols + c) * G + g] = D;
+            continue;
+        }
+        s = s + float(D) * (wscales[(size_t(quad) * G + g) * 4 + L] * as[size_t(r) * G + g]);
+    }
+    if (dots) return;
+    if (bias && n < n_rows) s = s + bias[n];
+    float *o = out + size_t(r) * ld_out + c;
+    *o = accumulate ? *o + s : s;
+}
+
 }  // namespace
+
+int launch_t2(const ProductArgs &a, hipStream_t s)
+{
+    const fg_table *t = a.t;
+    const int M = int(a.rows), K = int(t->cols), G = int(t->groups);
+    const int col_begin = int(a.quad_begin * 4), ncols = int((a.quad_end - a.quad_begin) * 4);
+    int8_t *q = const_cast<int8_t *>(a.q);
+    const float *as = a.as;
+    const int32_t *corr = a.corr;
+    void *ws = nullptr;
+    int rc = FG_OK;
+    if (a.x) {  // quantize the f32 rows first (groups of 128)
+        const size_t qb = (size_t(M) * K + 255) / 256 * 256, sb = (size_t(M) * G * 4 + 255) / 256 * 256;
+        FG_HIP(hipMallocAsync(&ws, qb + 2 * sb, s));
+        q = static_cast<int8_t *>(ws);
+        float *sc = reinterpret_cast<float *>(static_cast<char *>(ws) + qb);
+        int32_t *co = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + qb + sb);
+        rc = launch_quantize_rows(a.x, size_t(M) * K, FG_T2B128, q, sc, co, s);
+        as = sc;
+        corr = co;
+    }
+    if (rc == FG_OK) {
+        const long n = long(M) * ncols;
+        t2_product_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint8_t *>(t->codes), t->scales, int(t->blocks),
+                                                                   G, K, int(t->rows), q, as, corr, M, col_begin, ncols, a.bias,
+                                                                   a.out, long(a.ld_out), a.accumulate, a.dots);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) rc = check_hip(e, "t2_product_kernel");
+    }
+    if (ws) {
+        hipError_t e = hipFreeAsync(ws, s);
+        if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
+    }
+    return rc;
+}
 
 int launch_gemm(const ProductArgs &a, hipStream_t s)
 {
     const fg_table *t = a.t;
-    if (t->dtype == FG_T2B128) return set_error(FG_ERR_FORMAT, "T2b128 products are not built on the GPU");
+    if (t->dtype == FG_T2B128) return launch_t2(a, s);
     const int M = int(a.rows), K = int(t->cols), G = int(t->groups);
     const int Mpad = (M + 63) / 64 * 64;
     // Workspace: levels (when the input is f32), scales, corrections, block-major scales.
@@ -213,6 +287,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
 int launch_product(const ProductArgs &a, hipStream_t s)
 {
     if (a.rows == 0 || a.quad_end <= a.quad_begin) return FG_OK;
+    if (a.t->dtype == FG_T2B128) return launch_t2(a, s);
     if (a.rows <= 4) return launch_matvec(a, s);
     return launch_gemm(a, s);
 }

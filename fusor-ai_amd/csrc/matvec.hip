@@ -548,7 +548,7 @@ int launch_matvec(const ProductArgs &a, hipStream_t s)
     const fg_table *t = a.t;
     const int rows = int(a.rows);
     if (rows < 1 || rows > 4) return set_error(FG_ERR_SHAPE, "the matrix-vector kernel takes 1 to 4 rows");
-    if (t->dtype == FG_T2B128) return set_error(FG_ERR_FORMAT, "T2b128 products are not built on the GPU");
+    if (t->dtype == FG_T2B128) return set_error(FG_ERR_FORMAT, "the matrix-vector kernel takes Q7b32, Q8b32 and Q4b32 tables");
     ProjParams p{};
     p.codes = t->codes;
     p.wscales = t->scales;

@@ -7,13 +7,15 @@ from oracle import oracle as O
 
 def synthetic_table(dtype, rows, cols, seed, scale_lo=1e-3, scale_hi=1e-2):
     """Reference bytes of a [rows, cols] table with i.i.d. codes and scales: Q7b32 levels uniform in
-    [-63, 63] (codes 1..127), Q8b32 in [-127, 127], Q4b32 nibbles 0..15; scales uniform in
-    [scale_lo, scale_hi]. Codes are i.i.d., so filling the quad layout directly is the same draw as
-    packing row by row. Padding rows keep zero codes and zero scales (tensor.rs:83-88)."""
+    [-63, 63] (codes 1..127), Q8b32 in [-127, 127], Q4b32 nibbles 0..15, T2b128 bit pairs 0..2;
+    scales uniform in [scale_lo, scale_hi]. Codes are i.i.d., so filling the quad layout directly is
+    the same draw as packing row by row. Padding rows keep zero codes and zero scales
+    (tensor.rs:83-88)."""
     rng = np.random.default_rng(seed)
     quads = (rows + 3) // 4
     blocks = cols // 32
-    qb = 128 // (2 if dtype == O.Q4B32 else 1)
+    groups = cols // O.group(dtype)
+    qb = 128 // {O.Q4B32: 2, O.T2B128: 4}.get(dtype, 1)
     codes = np.zeros((quads, blocks, qb), np.uint8)
     if dtype == O.Q7B32:
         codes[:] = rng.integers(1, 128, codes.shape, dtype=np.uint8)
@@ -21,9 +23,12 @@ def synthetic_table(dtype, rows, cols, seed, scale_lo=1e-3, scale_hi=1e-2):
         codes[:] = rng.integers(-127, 128, codes.shape, dtype=np.int16).astype(np.int8).view(np.uint8)
     elif dtype == O.Q4B32:
         codes[:] = rng.integers(0, 256, codes.shape, dtype=np.uint8)
+    elif dtype == O.T2B128:
+        pairs = rng.integers(0, 3, codes.shape + (4,), dtype=np.uint8)
+        codes[:] = pairs[..., 0] | pairs[..., 1] << 2 | pairs[..., 2] << 4 | pairs[..., 3] << 6
     else:
         raise ValueError(dtype)
-    scales = rng.uniform(scale_lo, scale_hi, (quads, blocks, 4)).astype(np.float32)
+    scales = rng.uniform(scale_lo, scale_hi, (quads, groups, 4)).astype(np.float32)
     pad = quads * 4 - rows
     if pad:
         # zero the padding lanes' codes in the last quad and their scales

@@ -9,7 +9,7 @@ from gpu_data import activations, encoded_table, synthetic_table
 
 pytestmark = pytest.mark.gpu
 
-PRODUCT_FORMATS = [O.Q7B32, O.Q8B32, O.Q4B32]
+PRODUCT_FORMATS = [O.Q7B32, O.Q8B32, O.Q4B32, O.T2B128]
 ALL_FORMATS = [O.Q7B32, O.Q8B32, O.Q4B32, O.T2B128]
 
 
@@ -221,12 +221,13 @@ def test_every_format_matches_the_dequantized_product(fk, dtype):
         x = pseudo_random(rows * width, 7 + rows).reshape(rows, width)
         got = gpu_product(fk, t, x, rows)
         assert same_bits(got, oracle_product(dtype, outputs, width, data, x, rows))
+        g = O.group(dtype)
         for r in range(rows):
             qx = np.empty(width)
-            for k in range(0, width, 32):
-                blk = x[r, k:k + 32]
+            for k in range(0, width, g):
+                blk = x[r, k:k + g]
                 sc = np.max(np.abs(blk)) / np.float32(127.0)
-                qx[k:k + 32] = (np.rint(blk / sc) * sc).astype(np.float32)
+                qx[k:k + g] = (np.rint(blk / sc) * sc).astype(np.float32)
             want = w @ qx
             assert np.all(np.abs(got[r, :outputs] - want) < 1e-4 * (1 + np.abs(want)))
 

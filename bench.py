@@ -34,6 +34,21 @@ METRIC = "int8 qmatvec weight GB/s (% HBM peak); Qwen2-0.5B-shape decode tokens/
 Q7B32, Q4B32, Q8B32 = 1, 2, 4
 
 
+def measured_traffic():
+    """HBM bytes per launch of the projection pass from the committed counter summary (two
+    rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, scaled by a copy of known size); None when
+    the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "proj_kernel_qwen2_0.5b_projections_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch = "):
+                    return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -357,8 +372,8 @@ def main():
                    "step_bytes": step_bytes, "step_GB_s": round(step_bytes / ms / 1e6, 1),
                    "greedy_token": token},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "matvec_kernel (the step's 121 projections)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "proj_kernel through fg_matmul (the decode step's 121 projections)",
                      "bytes_per_launch": round(mv_bytes / mv_launches), "us_per_launch": round(mv_ms * 1e3 / mv_launches, 3),
                      "by_shape": mv_detail},
         "cpu_baseline": cpu,

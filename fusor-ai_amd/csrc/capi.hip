@@ -240,6 +240,113 @@ int fg_matmul(const fg_table *t, const fg_input *in, size_t rows, size_t col_beg
     return launch_product(a, as_stream(stream));
 }
 
+int fg_qmatrix_create(size_t capacity, size_t cols, fg_table **out)
+{
+    if (!out) return set_error(FG_ERR_ARG, "fg_qmatrix_create: a null output handle");
+    *out = nullptr;
+    // QuantizedMatrix::reset (matmul.rs:47-53)
+    if (cols % 32) return set_error(FG_ERR_SHAPE, "rows of whole blocks");
+    if (capacity > (size_t(1) << 31) || cols > (size_t(1) << 20)) return set_error(FG_ERR_SHAPE, "matrix too large");
+    fg_table *t = new fg_table();
+    t->dtype = FG_Q7B32;
+    t->capacity = capacity;
+    t->max_cols = cols;
+    t->rows = 0;
+    t->cols = cols;
+    t->quads = 0;
+    t->blocks = t->groups = cols / 32;
+    t->code_bytes = 0;
+    const size_t quads = (capacity + 3) / 4;
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&t->codes), std::max<size_t>(quads * t->blocks * 128, 16));
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&t->scales), std::max<size_t>(quads * t->blocks * 16, 16));
+    if (e != hipSuccess) {
+        (void)hipFree(t->codes);
+        delete t;
+        return check_hip(e, "fg_qmatrix_create");
+    }
+    *out = t;
+    return FG_OK;
+}
+
+static int check_qmatrix(const fg_table *t, const char *who)
+{
+    if (!t) return set_error(FG_ERR_ARG, std::string(who) + ": a null matrix");
+    if (!t->capacity) return set_error(FG_ERR_FORMAT, std::string(who) + ": a model table, not a run-time matrix");
+    return FG_OK;
+}
+
+int fg_qmatrix_reset(fg_table *t, size_t cols)
+{
+    int rc = check_qmatrix(t, "fg_qmatrix_reset");
+    if (rc) return rc;
+    if (cols % 32) return set_error(FG_ERR_SHAPE, "rows of whole blocks");  // matmul.rs:48
+    if (cols > t->max_cols) return set_error(FG_ERR_SHAPE, "fg_qmatrix_reset: wider than the matrix was created for");
+    t->rows = 0;
+    t->cols = cols;
+    t->quads = 0;
+    t->blocks = t->groups = cols / 32;
+    t->code_bytes = 0;
+    return FG_OK;
+}
+
+int fg_qmatrix_extend(fg_table *t, size_t rows, void *stream)
+{
+    int rc = check_qmatrix(t, "fg_qmatrix_extend");
+    if (rc) return rc;
+    hipStream_t s = as_stream(stream);
+    if (rows > (size_t(1) << 31) - t->rows) return set_error(FG_ERR_SHAPE, "matrix too large");
+    if (rows > t->capacity - t->rows) {
+        // Grow like the reference's Vec: the rows so far are a prefix of the layout (quad-major),
+        // so they move with one copy. The old storage is freed once the stream has drained.
+        const size_t capacity = std::max(t->capacity * 2, t->rows + rows);
+        const size_t quads = (capacity + 3) / 4, used = (t->rows + 3) / 4, blocks = t->max_cols / 32;
+        int8_t *codes = nullptr;
+        float *scales = nullptr;
+        hipError_t e = hipMalloc(reinterpret_cast<void **>(&codes), quads * blocks * 128);
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&scales), quads * blocks * 16);
+        if (e == hipSuccess) e = hipMemcpyAsync(codes, t->codes, used * t->blocks * 128, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(scales, t->scales, used * t->blocks * 16, hipMemcpyDeviceToDevice, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            (void)hipFree(codes);
+            (void)hipFree(scales);
+            return check_hip(e, "fg_qmatrix_extend");
+        }
+        (void)hipFree(t->codes);
+        (void)hipFree(t->scales);
+        t->codes = codes;
+        t->scales = scales;
+        t->capacity = capacity;
+    }
+    const size_t first = t->rows, last = (t->rows + rows + 3) / 4 * 4;
+    rc = launch_qmatrix_clear(t, first, last, s);
+    if (rc) return rc;
+    t->rows += rows;
+    t->quads = (t->rows + 3) / 4;
+    t->code_bytes = t->quads * t->blocks * 128;
+    return FG_OK;
+}
+
+int fg_qmatrix_set_rows(fg_table *t, size_t row, size_t count, const float *values, void *stream)
+{
+    int rc = check_qmatrix(t, "fg_qmatrix_set_rows");
+    if (rc) return rc;
+    if (row > t->rows || count > t->rows - row) return set_error(FG_ERR_SHAPE, "fg_qmatrix_set_rows: rows past the matrix");
+    if (!values && count) return set_error(FG_ERR_ARG, "fg_qmatrix_set_rows: null values");
+    if (reinterpret_cast<uintptr_t>(values) & 15) return set_error(FG_ERR_ARG, "fg_qmatrix_set_rows: values must be 16-byte aligned");
+    return launch_qmatrix_set(t, row, count, 0, t->blocks, values, t->cols, as_stream(stream));
+}
+
+int fg_qmatrix_set_block(fg_table *t, size_t row, size_t block, const float *values, void *stream)
+{
+    int rc = check_qmatrix(t, "fg_qmatrix_set_block");
+    if (rc) return rc;
+    if (row >= t->rows || block >= t->blocks) return set_error(FG_ERR_SHAPE, "fg_qmatrix_set_block: a block past the matrix");
+    if (!values) return set_error(FG_ERR_ARG, "fg_qmatrix_set_block: null values");
+    if (reinterpret_cast<uintptr_t>(values) & 15) return set_error(FG_ERR_ARG, "fg_qmatrix_set_block: values must be 16-byte aligned");
+    return launch_qmatrix_set(t, row, 1, block, 1, values, 32, as_stream(stream));
+}
+
 int fg_matmul_dots(const fg_table *t, const fg_input *in, size_t rows, size_t col_begin, size_t col_end, int32_t *dots, void *stream)
 {
     int rc = check_product(t, in, rows, col_begin, col_end, "fg_matmul_dots");

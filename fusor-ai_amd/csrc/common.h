@@ -50,6 +50,9 @@ struct fg_table {
     int8_t *codes;   // device layout, quads * blocks * quad_bytes bytes
     float *scales;   // quads * groups * 4
     size_t code_bytes;
+    // A run-time matrix (QuantizedMatrix): room for `capacity` rows of `max_cols` values; `rows`
+    // and `cols` are the rows appended so far and the current width. 0 for a model's table.
+    size_t capacity, max_cols;
 };
 
 namespace fg {
@@ -110,6 +113,9 @@ int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint
 int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s);
 int launch_quantize_rows(const float *x, size_t count, int dtype, int8_t *q, float *scales, int32_t *corr,
                          hipStream_t s);
+int launch_qmatrix_clear(fg_table *t, size_t first, size_t last, hipStream_t s);
+int launch_qmatrix_set(fg_table *t, size_t first, size_t count, size_t b0, size_t nb, const float *values, size_t ld,
+                       hipStream_t s);
 
 // One product: rows of int8 levels (q, scales, corrections) or f32 rows x quantized in-kernel.
 struct ProductArgs {

@@ -204,7 +204,72 @@ __global__ void quantize_rows_kernel(const float *__restrict__ x, size_t groups,
     }
 }
 
+// QuantizedMatrix::extend (matmul.rs:66-72): rows [first, last) to the reference's zero codes
+// (u = 0, stored as the level -64) and zero scales. One thread per (row, block).
+__global__ void qmatrix_clear_kernel(int8_t *__restrict__ codes, float *__restrict__ scales, size_t first, size_t last,
+                                     size_t blocks)
+{
+    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= (last - first) * blocks) return;
+    const size_t row = first + id / blocks, b = id % blocks, quad = row / 4;
+    const int lane = int(row % 4);
+    int4 *dst = reinterpret_cast<int4 *>(codes + (quad * blocks + b) * 128 + lane * 32);
+    const int v = int(0xC0C0C0C0u);
+    dst[0] = make_int4(v, v, v, v);
+    dst[1] = make_int4(v, v, v, v);
+    scales[(quad * blocks + b) * 4 + lane] = 0.0f;
+}
+
+// QuantizedMatrix::set_block (matmul.rs:77-90) for blocks [b0, b0 + nb) of rows
+// [first, first + count): the block's scale (absmax / 63, 1 for a zero block) and its Q7b32
+// levels (round ties to even, clamped to ±63), stored signed. values[r * ld + j * 32 + k] is
+// value k of block b0 + j of row first + r. One thread per (row, block).
+__global__ void qmatrix_set_kernel(int8_t *__restrict__ codes, float *__restrict__ scales, size_t first, size_t count,
+                                   size_t b0, size_t nb, size_t blocks, const float *__restrict__ values, size_t ld)
+{
+    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= count * nb) return;
+    const size_t r = id / nb, j = id % nb;
+    const size_t row = first + r, b = b0 + j, quad = row / 4;
+    const int lane = int(row % 4);
+    float x[32];
+    const float4 *src = reinterpret_cast<const float4 *>(values + r * ld + j * 32);
+    for (int i = 0; i < 8; i++) {
+        const float4 f = src[i];
+        x[4 * i] = f.x;
+        x[4 * i + 1] = f.y;
+        x[4 * i + 2] = f.z;
+        x[4 * i + 3] = f.w;
+    }
+    uint8_t u[128];
+    const float scale = quantize_group(FG_Q7B32, x, 32, u);
+    int *dst = reinterpret_cast<int *>(codes + (quad * blocks + b) * 128 + lane * 32);
+    for (int i = 0; i < 8; i++)
+        dst[i] = pack4(int(u[4 * i]) - 64, int(u[4 * i + 1]) - 64, int(u[4 * i + 2]) - 64, int(u[4 * i + 3]) - 64);
+    scales[(quad * blocks + b) * 4 + lane] = scale;
+}
+
 }  // namespace
+
+int launch_qmatrix_clear(fg_table *t, size_t first, size_t last, hipStream_t s)
+{
+    const size_t n = (last - first) * t->blocks;
+    if (n == 0) return FG_OK;
+    qmatrix_clear_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(t->codes, t->scales, first, last, t->blocks);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+int launch_qmatrix_set(fg_table *t, size_t first, size_t count, size_t b0, size_t nb, const float *values, size_t ld,
+                       hipStream_t s)
+{
+    const size_t n = count * nb;
+    if (n == 0) return FG_OK;
+    qmatrix_set_kernel<<<unsigned((n + 127) / 128), 128, 0, s>>>(t->codes, t->scales, first, count, b0, nb, t->blocks,
+                                                                values, ld);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
 
 int launch_relayout(const uint8_t *ref_codes, fg_table *t, hipStream_t s)
 {

@@ -2,20 +2,25 @@
 
 The names follow the reference crate's public API (kernels/src/lib.rs:22-31): DType, Tensor,
 Table, Matrix, Vector, QuantFormat, QuantizedRows, Quantized, Input, quantize_rows, matmul,
-Linear, project_input, project_residual_input and the constants. Every computation runs in the
+Linear, project, project_input, project_residual, project_residual_input, conv.project_rows,
+QuantizedMatrix and the constants. Every computation runs in the
 HIP library libfusor_gpu.so through its C ABI (include/fusor_gpu.h); there is no CPU fallback.
 """
 
 from ._lib import Error, FormatError, GpuError, ShapeError, lib
-from .linear import COLUMN_ALIGN, NARROW_COLUMN_ALIGN, Ctx, Linear, project_input, project_residual_input
-from .matmul import ROWS_PER_CALL, Input, Quantized, QuantizedRows, matmul, matmul_dots, quantize_rows
+from .conv import Patches, project_rows
+from .linear import (COLUMN_ALIGN, NARROW_COLUMN_ALIGN, Ctx, Linear, SharedRows, project, project_input,
+                     project_residual, project_residual_input)
+from .matmul import (ROWS_PER_CALL, Input, Quantized, QuantizedMatrix, QuantizedRows, matmul, matmul_dots,
+                     quantize_rows)
 from .qwen2 import Qwen2, Shape
 from .tensor import BLOCK, QUAD, TERNARY_GROUP, DType, Matrix, QuantFormat, Table, Tensor, Vector, byte_len
 
 __all__ = [
     "BLOCK", "QUAD", "TERNARY_GROUP", "ROWS_PER_CALL", "COLUMN_ALIGN", "NARROW_COLUMN_ALIGN",
     "DType", "QuantFormat", "Tensor", "Table", "Matrix", "Vector", "byte_len",
-    "QuantizedRows", "Quantized", "Input", "quantize_rows", "matmul", "matmul_dots",
-    "Linear", "Ctx", "project_input", "project_residual_input", "Qwen2", "Shape",
+    "QuantizedRows", "QuantizedMatrix", "Quantized", "Input", "quantize_rows", "matmul", "matmul_dots",
+    "Linear", "Ctx", "SharedRows", "project", "project_input", "project_residual", "project_residual_input",
+    "Patches", "project_rows", "Qwen2", "Shape",
     "Error", "FormatError", "ShapeError", "GpuError", "lib",
 ]

@@ -46,6 +46,11 @@ SIGNATURES = {
     "fg_table_read": (_I, [_P, _P, _P]),
     "fg_encode": (_I, [_I, _S, _S, _P, _P, _P]),
     "fg_dequantize_row": (_I, [_P, _S, _P, _P]),
+    "fg_qmatrix_create": (_I, [_S, _S, ctypes.POINTER(_P)]),
+    "fg_qmatrix_reset": (_I, [_P, _S]),
+    "fg_qmatrix_extend": (_I, [_P, _S, _P]),
+    "fg_qmatrix_set_rows": (_I, [_P, _S, _S, _P, _P]),
+    "fg_qmatrix_set_block": (_I, [_P, _S, _S, _P, _P]),
     "fg_quantize_rows": (_I, [_P, _S, _I, _P, _P, _P, _P]),
     "fg_matmul": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P, _S, _I, _P]),
     "fg_matmul_dots": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P]),

@@ -67,6 +67,31 @@ class Linear:
         return self.project(inp, range(0, self.matrix().rows))
 
 
+class SharedRows:
+    """linear.rs:22-27: the first `rows` rows of a shared activation buffer (a device f32
+    tensor)."""
+
+    def __init__(self, values, rows):
+        self.values, self.rows = values, rows
+
+
+def _prepare(linear, rows, quant):
+    """linear.rs:145-153: the rows as the linear's input, quantized when its weights are."""
+    m = linear.matrix()
+    return quant.input(m, rows.values.reshape(-1)[:rows.rows * m.cols])
+
+
+def project(ctx, linear, rows, quant, out):
+    """linear.rs:100-111: this thread's share of the columns of rows·Wᵀ + b into out [rows,
+    outputs], the rows quantized into `quant` (a QuantizedRows)."""
+    project_input(ctx, linear, _prepare(linear, rows, quant), out)
+
+
+def project_residual(ctx, linear, rows, residual, quant):
+    """linear.rs:121-132: residual[:, cols] += rows·Wᵀ + b for this thread's share."""
+    project_residual_input(ctx, linear, _prepare(linear, rows, quant), residual)
+
+
 def project_input(ctx, linear, x, out):
     """This thread's share of the columns of x·Wᵀ + b into out [rows, outputs] (linear.rs:112-119)."""
     outputs = linear.matrix().rows

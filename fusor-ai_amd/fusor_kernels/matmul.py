@@ -8,7 +8,7 @@ import ctypes
 
 from . import _lib
 from ._lib import FgInput, ShapeError, check, lib, ptr, stream_handle
-from .tensor import QUAD, QuantFormat
+from .tensor import BLOCK, QUAD, DType, QuantFormat
 
 ROWS_PER_CALL = 64  # matmul.rs:407
 
@@ -72,6 +72,61 @@ class QuantizedRows:
         self.corrections = torch.empty(n // g, dtype=torch.int32, device=x.device)
         quantize_rows(x.reshape(-1), fmt, self.quants, self.scales, self.corrections)
         return Input(quant=Quantized(fmt, self.quants, self.scales, self.corrections))
+
+
+class QuantizedMatrix:
+    """QuantizedMatrix (matmul.rs:35-102): a Q7b32 matrix quantized at run time, row by row (an
+    attention's keys and values), on the device; `matrix()` multiplies like a model's weights."""
+
+    def __init__(self, capacity=256, max_cols=4096):
+        from .tensor import Table
+        handle = ctypes.c_void_p()
+        check(lib().fg_qmatrix_create(capacity, max_cols, ctypes.byref(handle)))
+        self.table = Table.__new__(Table)
+        self.table.handle, self.table._dtype = handle, DType.Q7b32
+        self.table.rows, self.table.cols = 0, max_cols
+
+    def reset(self, cols):
+        """Empties it for rows of `cols` values, a multiple of BLOCK."""
+        if cols % BLOCK:
+            raise ShapeError("rows of whole blocks")
+        check(lib().fg_qmatrix_reset(self.table.handle, cols))
+        self.table.rows, self.table.cols = 0, cols
+
+    def extend(self, rows):
+        """Appends `rows` rows, every block of which `set_block` then writes once."""
+        check(lib().fg_qmatrix_extend(self.table.handle, rows, stream_handle()))
+        self.table.rows += rows
+
+    def push(self, row):
+        """Appends `row` (a device f32 tensor of cols values)."""
+        if row.numel() != self.table.cols:
+            raise ShapeError("a row of the matrix's width")
+        index = self.table.rows
+        self.extend(1)
+        self.set_rows(index, row)
+
+    def set_rows(self, first, values):
+        """Rows first.. from a device f32 tensor of whole rows (every block of each row)."""
+        count = values.numel() // self.table.cols
+        check(lib().fg_qmatrix_set_rows(self.table.handle, first, count, ptr(values), stream_handle()))
+
+    def set_block(self, row, block, values):
+        """Block `block` of row `row` from 32 device f32 values."""
+        if values.numel() != BLOCK:
+            raise ShapeError("a block of 32 values")
+        check(lib().fg_qmatrix_set_block(self.table.handle, row, block, ptr(values), stream_handle()))
+
+    @property
+    def rows(self):
+        return self.table.rows
+
+    @property
+    def cols(self):
+        return self.table.cols
+
+    def matrix(self):
+        return self.table.matrix()
 
 
 def _check_input(weights, x):

@@ -78,6 +78,26 @@ int fg_encode(int dtype, size_t rows, size_t cols, const float *values, void *by
 /* Matrix::dequantize_row (tensor.rs:247-271): row `row` as f32 into device `out` (cols long). */
 int fg_dequantize_row(const fg_table *table, size_t row, float *out, void *stream);
 
+/* ---------------------------------------------------------- run-time Q7b32 matrices */
+
+/* QuantizedMatrix (matmul.rs:35-102): a Q7b32 matrix quantized at run time, row by row (an
+ * attention's keys and values), created with room for `capacity` rows of up to `cols` values
+ * (it grows past them). The handle is a table: fg_matmul, fg_dequantize_row, fg_table_read and fg_table_free take it, and
+ * its Matrix is the rows appended so far. Created empty, `cols` wide (reset(cols), matmul.rs:47-53). */
+int fg_qmatrix_create(size_t capacity, size_t cols, fg_table **out);
+/* QuantizedMatrix::reset (matmul.rs:47-53): no rows, `cols` (whole blocks, at most the width it
+ * was created with) values per row. */
+int fg_qmatrix_reset(fg_table *matrix, size_t cols);
+/* QuantizedMatrix::extend (matmul.rs:66-72): `rows` more rows, zero codes and scales until set.
+ * Past the capacity the storage grows (doubling) and moves: the call then waits for `stream`,
+ * and work on other streams that reads the matrix must be ordered before it. */
+int fg_qmatrix_extend(fg_table *matrix, size_t rows, void *stream);
+/* QuantizedMatrix::push / set_block for whole rows (matmul.rs:56-64,77-90): rows
+ * [row, row + count), already appended, from device f32 `values` [count][cols]. */
+int fg_qmatrix_set_rows(fg_table *matrix, size_t row, size_t count, const float *values, void *stream);
+/* QuantizedMatrix::set_block (matmul.rs:77-90): block `block` of row `row` from 32 device f32. */
+int fg_qmatrix_set_block(fg_table *matrix, size_t row, size_t block, const float *values, void *stream);
+
 /* ------------------------------------------------------------------------ activations */
 
 /* quantize_rows (matmul.rs:233-257): `count` device f32 values, whole groups of the weight

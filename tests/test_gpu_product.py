@@ -288,3 +288,50 @@ def test_zero_rows_and_empty_ranges(fk):
     t = table(fk, O.Q7B32, 8, 64, data)
     x = activations(2, 64, seed=1)
     assert gpu_product(fk, t, x, 2, cols=range(4, 4)).shape == (2, 0)
+
+
+# ------------------------------------------------------------------------ golden vectors
+
+def _golden(name):
+    import os
+    with np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("name,dtype", [("Q7b32", O.Q7B32), ("Q4b32", O.Q4B32), ("T2b128", O.T2B128),
+                                        ("Q8b32", O.Q8B32)])
+def test_golden_lcg_vectors_on_the_gpu(fk, name, dtype):
+    """tests/golden/lcg_25x128.npz: levels, scales, corrections, group accumulators and f32
+    outputs of the reference test's inputs (matmul.rs:809-843), bit for bit."""
+    import torch
+    g = _golden("lcg_25x128.npz")
+    t = table(fk, dtype, 25, 128, g[f"{name}/table"])
+    assert np.array_equal(t.reference_bytes(), g[f"{name}/table"])
+    for rows in (1, 3, 8, 11):
+        p = f"{name}/rows{rows}/"
+        x = g[p + "x"]
+        n, grp = x.size, O.group(dtype)
+        q = torch.empty(n, dtype=torch.int8, device="cuda")
+        s = torch.empty(n // grp, dtype=torch.float32, device="cuda")
+        c = torch.empty(n // grp, dtype=torch.int32, device="cuda")
+        fk.quantize_rows(dev(x), fk.QuantFormat(dtype), q, s, c)
+        assert np.array_equal(host(q), g[p + "q"])
+        assert same_bits(host(s), g[p + "scales"])
+        assert np.array_equal(host(c), g[p + "corrections"])
+        assert same_bits(gpu_product(fk, t, x, rows), g[p + "out"])
+        assert np.array_equal(gpu_product(fk, t, x, rows, dots=True), g[p + "dots"])
+
+
+@pytest.mark.parametrize("name,dtype", [("Q7b32", O.Q7B32), ("Q8b32", O.Q8B32)])
+def test_golden_single_matvec_digest_on_the_gpu(fk, name, dtype):
+    """tests/golden/matvec_4864x896_seed0.npz: the 4864 x 896 seed-0 matvec's outputs and
+    accumulators by digest."""
+    import hashlib
+    g = _golden("matvec_4864x896_seed0.npz")
+    data = synthetic_table(dtype, 4864, 896, seed=0)
+    t = table(fk, dtype, 4864, 896, data)
+    x = activations(1, 896, seed=0)
+    out = np.ascontiguousarray(gpu_product(fk, t, x, 1), np.float32)
+    assert hashlib.sha256(out.tobytes()).digest() == g[f"{name}/out_sha256"].tobytes()
+    dots = np.ascontiguousarray(gpu_product(fk, t, x, 1, dots=True), np.int32)
+    assert hashlib.sha256(dots.tobytes()).digest() == g[f"{name}/dots_sha256"].tobytes()

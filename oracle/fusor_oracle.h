@@ -10,6 +10,25 @@
  * Arithmetic rules it keeps: IEEE f32 division and sqrt, ties-to-even rounding, no fused
  * multiply-add anywhere (built with -ffp-contract=off), saturating float->int casts, float sums
  * in index order from -0.0.
+ *
+ * What pins each part (tests/test_oracle.py, tests/test_golden.py); the reference is Rust and
+ * cannot be built or run here, so nothing is pinned by running it:
+ *   layout codec, encode, dequantize_row: the reference's known answers (the ternary byte
+ *     0b0001_1000 of tensor.rs:319-330, the subnormal row [127, 64] of matmul.rs:845-856), the
+ *     documented position rule, pack/unpack identity, the one-step error bound of
+ *     tensor.rs:287-317 and the quantizers' closed forms;
+ *   quantize_rows: the closed form (IEEE division, ties-to-even) recomputed in numpy, brute
+ *     force on tiny inputs, the invariant sum((u - zp) q) == corr + sum(u q);
+ *   matmul: every int32 group accumulator against an int64 brute force; the f32 sums against a
+ *     sequential, unfused numpy evaluation and an FMA variant that must differ; the reference
+ *     test's own f64 tolerance 1e-4 (1 + |want|) on its own inputs (matmul.rs:809-843);
+ *   exp, silu, rms_norm, softmax, rotary angles: closed forms and f64 within stated bounds;
+ *   rng: SplitMix64's published first output and xoshiro256**'s definition;
+ *   qwen2 layer and step: an independent f64 evaluation of the same model within the
+ *     reference's own tolerance for a Q7b32 stack (3e-2 relative L2, blocks/tests/stacks.rs:49-55).
+ *     Their f32 operation order (attention sums, norms, softmax) follows the cited reference
+ *     code but is parity unpinned at the bit level: no fixture or known answer of the
+ *     reference fixes those bits.
  */
 #ifndef FUSOR_ORACLE_H
 #define FUSOR_ORACLE_H

@@ -76,6 +76,36 @@ __device__ __forceinline__ int dot4(int a, int b, int acc) { return __builtin_am
 
 // The partner lane's value in pairs (lane ^ 1), through DPP.
 __device__ __forceinline__ int xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+// lane ^ 2 within a quad, and the mirror lane within 8 (lane ^ 7), through DPP.
+__device__ __forceinline__ int xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ int mirror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
+
+// Reductions over aligned groups of 8 lanes (every lane gets the group's result): after the two
+// quad steps each quad holds its own result, and the mirror exchanges the two quads.
+__device__ __forceinline__ float max8(float v)
+{
+    v = fmaxf(v, __int_as_float(xor1(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(xor2(__float_as_int(v))));
+    return fmaxf(v, __int_as_float(mirror8(__float_as_int(v))));
+}
+__device__ __forceinline__ int sum8(int v)
+{
+    v += xor1(v);
+    v += xor2(v);
+    return v + mirror8(v);
+}
+// Sum over the wave, in no particular order: groups of 8 through DPP, then the eight group
+// results read out and added.
+__device__ __forceinline__ float wave_sum_unordered(float v)
+{
+    v = v + __int_as_float(xor1(__float_as_int(v)));
+    v = v + __int_as_float(xor2(__float_as_int(v)));
+    v = v + __int_as_float(mirror8(__float_as_int(v)));
+    float s = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 64; g += 8) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), g));
+    return s;
+}
 
 // Activation quantization of one value at scale d (scalar.rs:57-66): ties-to-even rounding of the
 // IEEE quotient, clamped to ±127 in float, NaN to 0 (Rust's saturating cast).

@@ -7,10 +7,12 @@
 //   s = +0;  for g in order:  s = fl(s + fl(fl((float)D_g) · fl(ws[n,g] · as[r,g])))
 // then the bias (linear.rs:63-68) and, for residual projections, h = fl(h + y) (linear.rs:134-143).
 //
-// Mapping. A workgroup owns `qpw` consecutive quads (4 output rows each) and all of their blocks:
-// a contiguous run of the table (two runs for the gated feed-forward's gate and up tables). Its
-// four waves stream the run in 1 KiB chunks (64 lanes x 16 B, fully coalesced 128-bit loads),
+// Mapping. A workgroup owns `qpw` quads (4 output rows each; consecutive, or a rotary pair D/8
+// quads apart) and all of their blocks (in two tables for the gated feed-forward's gate and up).
+// Its four waves stream them in 1 KiB chunks (64 lanes x 16 B, coalesced 128-bit loads),
 // `kBatch` chunks per wave in flight, the next batch issued before the current one is consumed.
+// Small workgroups (a few quads, about 16 KiB of codes) spread a small table over every CU: a
+// CU keeps a bounded number of reads in flight, so a large share per CU costs round trips.
 // The first batch is issued before the activations are staged, so the prologue (a copy, an
 // in-kernel quantization, or an RMSNorm followed by the quantization) runs under the weights'
 // memory latency. Every lane turns its 16 bytes into a partial int32 dot with v_dot4 against the
@@ -21,7 +23,9 @@
 // Epilogues: store (with bias, or added to a residual row, optionally each workgroup's greedy
 // candidate); QKV (bias, rotary embedding by halves of the query and key heads, the key and value
 // heads kept in the cache: rope_half ops.rs:77-85, KvCache::keep transformer.rs:166-180); SwiGLU
-// (silu(gate)·up quantized per group of 32 for the down projection, layer.rs:321-341).
+// (silu(gate)·up as f32, layer.rs:321-341, which the down projection quantizes as its input).
+#include <algorithm>
+
 #include "common.h"
 #include "proj.h"
 
@@ -32,79 +36,65 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ int dot16(int4 w, int4 a) { return dot4(w.w, a.w, dot4(w.z, a.z, dot4(w.y, a.y, dot4(w.x, a.x, 0)))); }
 
-// Quantize `n` LDS floats (a multiple of 32) into levels / scales / corrections, 8 lanes per group
-// (quantize_rows, matmul.rs:233-257). Every thread of the block calls it.
-__device__ void quantize_lds_to(const float *v, int n, int zp, int8_t *q, float *scales, int32_t *corr)
-{
-    const int sub = threadIdx.x & 7;
-    const int groups = n / 32;
-    const int per_round = kThreads / 8;
-    for (int g0 = 0; g0 < groups; g0 += per_round) {
-        const int g = g0 + int(threadIdx.x >> 3);
-        const bool active = g < groups;
-        float x0 = 0, x1 = 0, x2 = 0, x3 = 0;
-        if (active) {
-            const float4 f = *reinterpret_cast<const float4 *>(v + g * 32 + sub * 4);
-            x0 = f.x, x1 = f.y, x2 = f.z, x3 = f.w;
-        }
-        float amax = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-        amax = fmaxf(0.0f, amax);
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        const float d = group_scale(amax, 127.0f);
-        const int l0 = quantize_level(x0, d), l1 = quantize_level(x1, d), l2 = quantize_level(x2, d), l3 = quantize_level(x3, d);
-        int sum = l0 + l1 + l2 + l3;
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
-        if (active) {
-            reinterpret_cast<int *>(q)[g * 8 + sub] = pack4(l0, l1, l2, l3);
-            if (sub == 0) {
-                scales[g] = d;
-                corr[g] = -zp * sum;
-            }
-        }
-    }
-}
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Σ t[g·stride] for g in 0..n, added in index order from +0; loads issued 16 at a time so that
-// the dependent additions do not wait on each load.
-__device__ __forceinline__ float ordered_sum(const float *t, int n, int stride)
+// Σ t[g] for g in 0..n, added in index order from +0. `t` is 16-byte aligned and readable up to n
+// rounded up to 4. Whole runs of 32 terms come in eight 128-bit reads, the next run in flight
+// while the current one is added (straight-line adds, no per-term branch); then the tail.
+__device__ __forceinline__ float ordered_sum(const float *t, int n)
 {
+    constexpr int V = 8;  // 128-bit reads per run
+    const v4f *t4 = reinterpret_cast<const v4f *>(t);
+    const int runs = n / (4 * V);
     float s = 0.0f;
-    int g = 0;
-    for (; g + 16 <= n; g += 16) {
-        float v[16];
+    v4f cur[V], nxt[V];
+    if (runs > 0) {
 #pragma unroll
-        for (int k = 0; k < 16; k++) v[k] = t[(g + k) * stride];
-#pragma unroll
-        for (int k = 0; k < 16; k++) s = s + v[k];
+        for (int k = 0; k < V; k++) cur[k] = t4[k];
     }
-    for (; g < n; g++) s = s + t[g * stride];
+    for (int c = 0; c < runs; c++) {
+        if (c + 1 < runs) {
+#pragma unroll
+            for (int k = 0; k < V; k++) nxt[k] = t4[(c + 1) * V + k];
+        }
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            s = s + cur[k].x;
+            s = s + cur[k].y;
+            s = s + cur[k].z;
+            s = s + cur[k].w;
+        }
+#pragma unroll
+        for (int k = 0; k < V; k++) cur[k] = nxt[k];
+    }
+    const int g0 = runs * 4 * V, rest4 = (n - g0 + 3) / 4;
+    if (rest4 > 0) {
+#pragma unroll
+        for (int k = 0; k < V; k++) cur[k] = t4[runs * V + min(k, rest4 - 1)];
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            // s is never -0 (it starts at +0), so adding +0 for a term past the end is no change
+            const int g = g0 + 4 * k;
+            s = s + (g < n ? cur[k].x : 0.0f);
+            s = s + (g + 1 < n ? cur[k].y : 0.0f);
+            s = s + (g + 2 < n ? cur[k].z : 0.0f);
+            s = s + (g + 3 < n ? cur[k].w : 0.0f);
+        }
+    }
     return s;
-}
-
-__device__ float block_sum256(float v, float *red)
-{
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
 // The activations' global loads, issued before the first weight batch: vector loads complete in
 // order, so loads issued after the weights would wait for them.
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct StageRegs {
     v4i v0, v1, v2, v3;
     float s0, s1, s2, s3;
     int c0, c1, c2, c3;
-    v4f f0, f1, f2, f3;
-    float x[8], w[8];
+    v4f f0, f1, f2, f3;  // f32 rows (IN_F32) or the row to normalize (IN_NORM)
+    v4f f4, f5, f6, f7;  // more f32 rows (IN_F32)
+    v4f w0, w1, w2, w3;  // the RMSNorm weight (IN_NORM)
 };
 
 
@@ -135,13 +125,23 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
         g.f1 = x4[min(tid + kThreads, n4 - 1)];
         g.f2 = x4[min(tid + 2 * kThreads, n4 - 1)];
         g.f3 = x4[min(tid + 3 * kThreads, n4 - 1)];
+        g.f4 = x4[min(tid + 4 * kThreads, n4 - 1)];
+        g.f5 = x4[min(tid + 5 * kThreads, n4 - 1)];
+        g.f6 = x4[min(tid + 6 * kThreads, n4 - 1)];
+        g.f7 = x4[min(tid + 7 * kThreads, n4 - 1)];
     } else {
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = min(tid + k * kThreads, K - 1);
-            g.x[k] = p.x[i];
-            g.w[k] = p.norm_w[i];
-        }
+        // one row of at most 4 · 256 float4s (K <= 4096, checked on the host)
+        const v4f *x4 = reinterpret_cast<const v4f *>(p.x);
+        const v4f *w4 = reinterpret_cast<const v4f *>(p.norm_w);
+        const int n4 = K / 4;
+        g.f0 = x4[min(tid, n4 - 1)];
+        g.f1 = x4[min(tid + kThreads, n4 - 1)];
+        g.f2 = x4[min(tid + 2 * kThreads, n4 - 1)];
+        g.f3 = x4[min(tid + 3 * kThreads, n4 - 1)];
+        g.w0 = w4[min(tid, n4 - 1)];
+        g.w1 = w4[min(tid + kThreads, n4 - 1)];
+        g.w2 = w4[min(tid + 2 * kThreads, n4 - 1)];
+        g.w3 = w4[min(tid + 3 * kThreads, n4 - 1)];
     }
 }
 
@@ -150,16 +150,10 @@ __device__ __forceinline__ void quantize8(v4f v, int zp, int grp, int8_t *q, flo
 {
     const int sub = threadIdx.x & 7;
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(0.0f, amax);
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    amax = max8(fmaxf(0.0f, amax));
     const float d = group_scale(amax, 127.0f);
     const int l0 = quantize_level(v.x, d), l1 = quantize_level(v.y, d), l2 = quantize_level(v.z, d), l3 = quantize_level(v.w, d);
-    int sum = l0 + l1 + l2 + l3;
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
+    const int sum = sum8(l0 + l1 + l2 + l3);
     reinterpret_cast<int *>(q)[grp * 8 + sub] = pack4(l0, l1, l2, l3);
     if (sub == 0) {
         scales[grp] = d;
@@ -200,24 +194,32 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         // 8 lanes per group of 32 (quantize_rows): thread t holds float4 t of the rows; every lane
         // of an 8-lane group is active together (the float4 count is a multiple of 8)
         const int n4 = R * K / 4;
-        if (tid < n4) quantize8(g.f0, p.zp, tid / 8, act_q, act_s, act_c);
-        if (tid + kThreads < n4) quantize8(g.f1, p.zp, (tid + kThreads) / 8, act_q, act_s, act_c);
-        if (tid + 2 * kThreads < n4) quantize8(g.f2, p.zp, (tid + 2 * kThreads) / 8, act_q, act_s, act_c);
-        if (tid + 3 * kThreads < n4) quantize8(g.f3, p.zp, (tid + 3 * kThreads) / 8, act_q, act_s, act_c);
-        for (int i = tid + 4 * kThreads; i < n4; i += kThreads)
+#define FG_Q8(v, k) \
+    if (tid + (k) * kThreads < n4) quantize8((v), p.zp, (tid + (k) * kThreads) / 8, act_q, act_s, act_c);
+        FG_Q8(g.f0, 0)
+        FG_Q8(g.f1, 1)
+        FG_Q8(g.f2, 2)
+        FG_Q8(g.f3, 3)
+        FG_Q8(g.f4, 4)
+        FG_Q8(g.f5, 5)
+        FG_Q8(g.f6, 6)
+        FG_Q8(g.f7, 7)
+#undef FG_Q8
+        for (int i = tid + 8 * kThreads; i < n4; i += kThreads)
             quantize8(reinterpret_cast<const v4f *>(p.x)[i], p.zp, i / 8, act_q, act_s, act_c);
     } else {
         // rms_norm (ops.rs:7-16): mean of squares, 1/sqrt(mean + eps), x·inverse·weight; then the
-        // quantization of the normed row
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = tid + k * kThreads;
-            if (i < K) nbuf[i] = g.x[k];
-        }
-        for (int i = tid + 8 * kThreads; i < K; i += kThreads) nbuf[i] = p.x[i];
-        __syncthreads();
+        // quantization of the normed row. Thread t holds float4s t, t + 256, ... of the row, so
+        // eight consecutive threads hold one group of 32.
+        const int n4 = K / 4;
         float total;
         if (EXACT) {
+            v4f *row = reinterpret_cast<v4f *>(nbuf);
+            if (tid < n4) row[tid] = g.f0;
+            if (tid + kThreads < n4) row[tid + kThreads] = g.f1;
+            if (tid + 2 * kThreads < n4) row[tid + 2 * kThreads] = g.f2;
+            if (tid + 3 * kThreads < n4) row[tid + 3 * kThreads] = g.f3;
+            __syncthreads();
             if (tid == 0) {
                 float s = -0.0f;  // dot_f32(row, row) in index order (arch/scalar.rs:340-342)
                 for (int i = 0; i < K; i += 32) {
@@ -238,19 +240,23 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             total = red[4];
         } else {
             float part = 0.0f;
-            for (int i = tid; i < K; i += kThreads) part = part + nbuf[i] * nbuf[i];
-            total = block_sum256(part, red);
+#define FG_SQ(v, k) \
+    if (tid + (k) * kThreads < n4) part = part + (((v).x * (v).x + (v).y * (v).y) + ((v).z * (v).z + (v).w * (v).w));
+            FG_SQ(g.f0, 0)
+            FG_SQ(g.f1, 1)
+            FG_SQ(g.f2, 2)
+            FG_SQ(g.f3, 3)
+#undef FG_SQ
+            part = wave_sum_unordered(part);
+            if ((tid & 63) == 0) red[tid >> 6] = part;
+            __syncthreads();
+            total = ((red[0] + red[1]) + red[2]) + red[3];
         }
         const float inverse = 1.0f / sqrtf(total / float(K) + p.eps);
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = tid + k * kThreads;
-            if (i < K) nbuf[i] = nbuf[i] * inverse * g.w[k];
-        }
-        for (int i = tid + 8 * kThreads; i < K; i += kThreads) nbuf[i] = nbuf[i] * inverse * p.norm_w[i];
-        __syncthreads();
-        quantize_lds_to(nbuf, K, p.zp, act_q, act_s, act_c);
+        if (tid < n4) quantize8(g.f0 * inverse * g.w0, p.zp, tid / 8, act_q, act_s, act_c);
+        if (tid + kThreads < n4) quantize8(g.f1 * inverse * g.w1, p.zp, (tid + kThreads) / 8, act_q, act_s, act_c);
+        if (tid + 2 * kThreads < n4) quantize8(g.f2 * inverse * g.w2, p.zp, (tid + 2 * kThreads) / 8, act_q, act_s, act_c);
+        if (tid + 3 * kThreads < n4) quantize8(g.f3 * inverse * g.w3, p.zp, (tid + 3 * kThreads) / 8, act_q, act_s, act_c);
     }
 }
 
@@ -261,61 +267,78 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NT = OUT == OUT_SWIGLU ? 2 : 1;  // tables streamed
     const int K = p.K, G = p.G, B = p.B;
-    const int qa = p.quad_begin + int(blockIdx.x) * p.qpw;
-    const int nq = min(p.qpw, p.quad_end - qa);
+    const int Gp = (G + 3) & ~3;  // terms per output, padded for 128-bit reads
+    const int qs = p.qstride;
+    const int base = p.quad_begin + int(blockIdx.x) / qs * qs * p.qpw + int(blockIdx.x) % qs;
+    const int nq = base < p.quad_end ? min(p.qpw, (p.quad_end - base + qs - 1) / qs) : 0;
+    if (nq <= 0) return;  // the host's grids leave none empty
     const int NW = p.qpw * 4;
+    auto output_of = [&](int nl) { return (base + (nl >> 2) * qs) * 4 + (nl & 3); };  // local -> column
     const ProjLayout lay = proj_layout(R, K, G, NW, IN, OUT);
     int8_t *act_q = reinterpret_cast<int8_t *>(smem);
     float *act_s = reinterpret_cast<float *>(smem + lay.off_s);      // [R][G]
     int32_t *act_c = reinterpret_cast<int32_t *>(smem + lay.off_c);  // [R][G]
     float *red = reinterpret_cast<float *>(smem + lay.off_red);      // [16]
     float *ybuf = reinterpret_cast<float *>(smem + lay.off_y);       // [NT (+1)][R][NW]
-    float *terms = reinterpret_cast<float *>(smem + lay.off_terms);  // [NT][R][G][NW]
+    float *terms = reinterpret_cast<float *>(smem + lay.off_terms);  // [NT][R][NW][Gp]
     float *nbuf = reinterpret_cast<float *>(smem + lay.off_n);       // [K] (IN_NORM)
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int QB = FMT == 8 ? 128 : 64;         // device bytes per quad block
     constexpr int QB_PER_CHUNK = 1024 / QB;         // quad blocks per 1 KiB chunk
     const int total_qb = nq * B;
-    const int per_table = (total_qb + QB_PER_CHUNK - 1) / QB_PER_CHUNK;
-    const int chunks = NT * per_table;
+    const int per_table = (total_qb + QB_PER_CHUNK - 1) / QB_PER_CHUNK;  // chunks per table
     const int L = FMT == 8 ? (lane >> 1) & 3 : lane & 3;
     const int h = FMT == 8 ? lane & 1 : 0;
     const int qb_in_chunk = FMT == 8 ? lane >> 3 : lane >> 2;
-    const int mine = chunks > wave ? (chunks - wave + 3) / 4 : 0;  // chunks of this wave
+    const int piece = FMT == 8 ? lane & 7 : lane & 3;  // this lane's 16 bytes of its quad block
+    // Chunk k of a wave is chunk wt + k·stride of table tb: with two tables, waves 0 and 2 stream
+    // the gate, 1 and 3 the up table.
+    constexpr int stride = 4 / NT;
+    const int tb = NT == 2 ? (wave & 1) : 0;
+    const int wt = NT == 2 ? (wave >> 1) : wave;
+    const int mine = per_table > wt ? (per_table - wt + stride - 1) / stride : 0;  // chunks of this wave
     const int batches = (mine + kBatch - 1) / kBatch;
+    const int8_t *codes = tb ? p.codes2 : p.codes;
+    const float *wsc = tb ? p.wscales2 : p.wscales;
+    // The lane's quad block (local quad ql, block blk) walks by `stride` chunks at a time: one
+    // division up front, then a quotient and a remainder step.
+    const int qb0 = wt * QB_PER_CHUNK + qb_in_chunk;
+    const int step_q = stride * QB_PER_CHUNK / B, step_r = stride * QB_PER_CHUNK - step_q * B;
+    struct Cursor {
+        int ql, blk;
+    };
+    auto advance = [&](Cursor &cu) {
+        cu.ql += step_q;
+        cu.blk += step_r;
+        if (cu.blk >= B) {
+            cu.blk -= B;
+            cu.ql++;
+        }
+    };
+    Cursor lcur{qb0 / B, qb0 % B};
+    Cursor ccur = lcur;
 
-    // Branch-free: every lane loads, from its own address when its chunk exists and from the
-    // run's first bytes otherwise (always in bounds), so the loads of a batch issue back to back
-    // with a single wait when consumed; `consume` skips what was not valid.
-    auto load = [&](int b, int4 *w, float *ws) {
+    // Branch-free: every lane loads, past the run's end from its last quad (always in bounds), so
+    // the loads of a batch issue back to back with a single wait when consumed; `consume` skips
+    // what was not valid. The cursor keeps blk < B, so only the quad needs the clamp.
+    auto load = [&](int4 *w, float *ws) {
 #pragma unroll
         for (int u = 0; u < kBatch; u++) {
-            const int c = wave + 4 * (b * kBatch + u);
-            const int tb = NT == 2 ? (c >= per_table) : 0;
-            const int cc = c - tb * per_table;
-            const int qb = cc * QB_PER_CHUNK + qb_in_chunk;
-            const bool ok = c < chunks && qb < total_qb;
-            const int8_t *codes = tb ? p.codes2 : p.codes;
-            const float *wsc = tb ? p.wscales2 : p.wscales;
-            const int ql = qb / B, blk = qb - ql * B;
-            const size_t coff = ok ? size_t(qa) * B * QB + size_t(cc) * 1024 + lane * 16 : size_t(qa) * B * QB;
-            const size_t soff = ok ? (size_t(qa + ql) * G + blk) * 4 + L : size_t(qa) * G * 4;
-            w[u] = *reinterpret_cast<const int4 *>(codes + coff);
-            ws[u] = wsc[soff];
+            const size_t quad = size_t(base + min(lcur.ql, nq - 1) * qs);
+            w[u] = *reinterpret_cast<const int4 *>(codes + (quad * B + lcur.blk) * QB + piece * 16);
+            ws[u] = wsc[(quad * G + lcur.blk) * 4 + L];
+            advance(lcur);
         }
     };
 
     auto consume = [&](int b, const int4 *w, const float *ws) {
 #pragma unroll
         for (int u = 0; u < kBatch; u++) {
-            const int c = wave + 4 * (b * kBatch + u);
-            if (c >= chunks) continue;  // uniform across the wave
-            const int tb = NT == 2 ? (c >= per_table) : 0;
-            const int cc = c - tb * per_table;
-            const int qb = cc * QB_PER_CHUNK + qb_in_chunk;
-            const bool valid = qb < total_qb;
-            const int ql = valid ? qb / B : 0, blk = valid ? qb - ql * B : 0;
+            const int ql = ccur.ql, blk = ccur.blk;
+            advance(ccur);
+            if (b * kBatch + u >= mine) continue;  // uniform across the wave
+            const bool valid = ql < nq;
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 int D;
@@ -324,20 +347,21 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
                     D = dot16(w[u], a);
                     D += xor1(D);  // the row-block's other half
                 } else {
-                    const int4 a0 = *reinterpret_cast<const int4 *>(act_q + r * K + blk * 32);
-                    const int4 a1 = *reinterpret_cast<const int4 *>(act_q + r * K + blk * 32 + 16);
+                    const int bb = blk;
+                    const int4 a0 = *reinterpret_cast<const int4 *>(act_q + r * K + bb * 32);
+                    const int4 a1 = *reinterpret_cast<const int4 *>(act_q + r * K + bb * 32 + 16);
                     const int4 lo = make_int4(w[u].x & 0x0F0F0F0F, w[u].y & 0x0F0F0F0F, w[u].z & 0x0F0F0F0F, w[u].w & 0x0F0F0F0F);
                     const int4 hi = make_int4((w[u].x >> 4) & 0x0F0F0F0F, (w[u].y >> 4) & 0x0F0F0F0F,
                                               (w[u].z >> 4) & 0x0F0F0F0F, (w[u].w >> 4) & 0x0F0F0F0F);
-                    D = dot16(lo, a0) + dot16(hi, a1) + act_c[r * G + blk];
+                    D = dot16(lo, a0) + dot16(hi, a1) + act_c[r * G + bb];
                 }
                 if (valid && h == 0) {
                     if (OUT == OUT_DOTS) {
-                        const int n = (qa + ql) * 4 + L;
+                        const int n = (base + ql * qs) * 4 + L;
                         p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * G + blk] = D;
                     } else {
                         const float scale = ws[u] * act_s[r * G + blk];
-                        terms[((tb * R + r) * G + blk) * NW + ql * 4 + L] = float(D) * scale;
+                        terms[((tb * R + r) * NW + ql * 4 + L) * Gp + blk] = float(D) * scale;
                     }
                 }
             }
@@ -348,21 +372,26 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     float sa[kBatch], sb[kBatch];
     StageRegs g;
     stage_issue<R, IN>(p, g);
-    // the residual row this workgroup adds to, read early (linear.rs:139-142)
+    // the residual row this workgroup adds to, read early (linear.rs:139-142); read whether or not
+    // it is added, so that no branch splits the loads before the weights' first batch
     float resid = 0.0f;
-    if (OUT == OUT_STORE && p.accumulate) {
+    if (OUT == OUT_STORE) {
         const int r = int(threadIdx.x) / NW, nl = int(threadIdx.x) - r * NW;
         const bool mine = r < R && nl < nq * 4;
-        resid = p.out[mine ? r * p.ld_out + (qa * 4 + nl - p.col_begin) : 0];
+        resid = p.out[mine ? r * p.ld_out + (output_of(nl) - p.col_begin) : 0];
     }
-    if (batches > 0) load(0, wa, sa);
+    // keep the activation loads ahead of the weights': loads return in order, and the prologue
+    // waits only for the activations
+    __builtin_amdgcn_sched_barrier(0);
+    load(wa, sa);  // every wave, in bounds even without chunks of its own
+    __builtin_amdgcn_sched_barrier(0);  // and all of them issued before the prologue's first wait
     stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
     __syncthreads();
     for (int b = 0; b < batches; b += 2) {
-        if (b + 1 < batches) load(b + 1, wb, sb);
+        if (b + 1 < batches) load(wb, sb);
         consume(b, wa, sa);
         if (b + 1 < batches) {
-            if (b + 2 < batches) load(b + 2, wa, sa);
+            if (b + 2 < batches) load(wa, sa);
             consume(b + 1, wb, sb);
         }
     }
@@ -374,9 +403,8 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         const int tb = i / (R * NW), rem = i - tb * R * NW;
         const int r = rem / NW, nl = rem - r * NW;
         if (nl >= nq * 4) continue;
-        const float *t = terms + (tb * R + r) * G * NW + nl;
-        float s = ordered_sum(t, G, NW);
-        const int n = qa * 4 + nl;
+        float s = ordered_sum(terms + ((tb * R + r) * NW + nl) * Gp, G);
+        const int n = output_of(nl);
         if (OUT != OUT_SWIGLU && p.bias && n < p.n_rows) s = s + p.bias[n];
         if (OUT == OUT_STORE) {
             float *o = p.out + r * p.ld_out + (n - p.col_begin);
@@ -394,7 +422,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             float best = 0.0f;
             int idx = -1;
             for (int nl = threadIdx.x; nl < nq * 4; nl += kThreads) {
-                const int n = qa * 4 + nl;
+                const int n = output_of(nl);
                 const float v = ybuf[nl];
                 if (n < p.n_rows && v == v && (idx < 0 || v > best)) {
                     best = v;
@@ -431,13 +459,14 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     }
     __syncthreads();
     if (OUT == OUT_QKV) {
-        // whole heads per workgroup: bias is in; rotate query and key heads, keep keys and values
+        // a rotary pair per workgroup (qstride = D/8, qpw = 2): outputs 0..3 are dimensions
+        // j0..j0+3 of a head, outputs 4..7 the same dimensions + D/2. The bias is in; query and key
+        // heads rotate by halves, key and value heads go to the cache.
         const int D = p.D, half = D / 2;
-        const int first_unit = qa * 4 / D;
-        for (int i = threadIdx.x; i < nq * 4 / 2; i += kThreads) {
-            const int u = i / half, j = i - u * half;
-            const int unit = first_unit + u;
-            float x = ybuf[u * D + j], y = ybuf[u * D + j + half];
+        const int unit = base * 4 / D, j0 = base * 4 - unit * D;
+        if (threadIdx.x < 4) {
+            const int j = j0 + int(threadIdx.x);
+            float x = ybuf[threadIdx.x], y = ybuf[4 + threadIdx.x];
             if (unit < p.heads + p.kv_heads) {
                 const float c = p.rope[j], sn = p.rope[half + j];
                 const float nx = x * c - y * sn;
@@ -457,11 +486,8 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             }
         }
     } else if (OUT == OUT_SWIGLU) {
-        // silu(gate)·up (layer.rs:321-341), quantized per group of 32 for the down projection
-        for (int nl = threadIdx.x; nl < nq * 4; nl += kThreads) ybuf[2 * NW + nl] = ref_silu(ybuf[nl]) * ybuf[NW + nl];
-        __syncthreads();
-        const int g0 = qa * 4 / 32;
-        quantize_lds_to(ybuf + 2 * NW, nq * 4, p.zp_out, p.q_out + g0 * 32, p.s_out + g0, p.c_out + g0);
+        // silu(gate)·up (layer.rs:321-341); the down projection quantizes the row
+        for (int nl = threadIdx.x; nl < nq * 4; nl += kThreads) p.act_out[output_of(nl)] = ref_silu(ybuf[nl]) * ybuf[NW + nl];
     }
 }
 
@@ -502,8 +528,7 @@ int dispatch_rows(const ProjParams &p, int rows, int in, bool dots, size_t smem,
     }
 }
 
-// The decoder's launches: 16 chunks per wave in flight where workgroups are few (one per head or
-// per 32 outputs), 8 where they are many.
+// The decoder's launches, in the reference's reduction order (exact) or with parallel f32 sums.
 template <int FMT, int IN, int OUT, int NB>
 int dispatch_exact(const ProjParams &p, bool exact, size_t smem, unsigned grid, hipStream_t s)
 {
@@ -522,21 +547,30 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     ProjParams p = p0;
     const int nq = p.quad_end - p.quad_begin;
     if (nq <= 0) return FG_OK;
-    const unsigned grid = unsigned((nq + p.qpw - 1) / p.qpw);
+    if (p.qstride < 1) p.qstride = 1;
+    const int span = p.qstride * p.qpw;
+    if (p.qstride > 1 && nq % span) return set_error(FG_ERR_SHAPE, "strided quads cover whole spans");
+    if (out == OUT_QKV && (p.qpw != 2 || p.qstride * 8 != p.D))
+        return set_error(FG_ERR_SHAPE, "the QKV epilogue takes one rotary pair per workgroup");
+    if (in == IN_NORM && p.K > 4 * 4 * kThreads) return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
+    const unsigned grid = p.qstride == 1 ? unsigned((nq + p.qpw - 1) / p.qpw) : unsigned(nq / span * p.qstride);
     const size_t smem = proj_smem(p, 1, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
     const bool q4 = dtype == FG_Q4B32;
     switch (out) {
     case OUT_QKV:
-        return q4 ? dispatch_exact<4, IN_NORM, OUT_QKV, 16>(p, exact, smem, grid, s)
-                  : dispatch_exact<8, IN_NORM, OUT_QKV, 16>(p, exact, smem, grid, s);
+        return q4 ? dispatch_exact<4, IN_NORM, OUT_QKV, 8>(p, exact, smem, grid, s)
+                  : dispatch_exact<8, IN_NORM, OUT_QKV, 8>(p, exact, smem, grid, s);
     case OUT_SWIGLU:
-        return q4 ? dispatch_exact<4, IN_NORM, OUT_SWIGLU, 16>(p, exact, smem, grid, s)
-                  : dispatch_exact<8, IN_NORM, OUT_SWIGLU, 16>(p, exact, smem, grid, s);
+        return q4 ? dispatch_exact<4, IN_NORM, OUT_SWIGLU, 8>(p, exact, smem, grid, s)
+                  : dispatch_exact<8, IN_NORM, OUT_SWIGLU, 8>(p, exact, smem, grid, s);
     default:
         if (in == IN_NORM)
             return q4 ? dispatch_exact<4, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s)
                       : dispatch_exact<8, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s);
+        if (in == IN_F32)
+            return q4 ? launch_one<4, 1, IN_F32, OUT_STORE, false, 8>(p, smem, grid, s)
+                      : launch_one<8, 1, IN_F32, OUT_STORE, false, 8>(p, smem, grid, s);
         return q4 ? launch_one<4, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s)
                   : launch_one<8, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s);
     }
@@ -574,11 +608,14 @@ int launch_matvec(const ProductArgs &a, hipStream_t s)
     if (nq <= 0) return FG_OK;
     const int in = a.x ? IN_F32 : IN_PREQ;
     const int out = a.dots ? OUT_DOTS : OUT_STORE;
-    // Quads per workgroup: enough workgroups to cover the chip, more quads per group when
-    // activations are quantized in-kernel (each group quantizes them once).
-    int qpw = in == IN_F32 ? nq / 512 : nq / 1024;
-    qpw = qpw < 1 ? 1 : (qpw > 16 ? 16 : qpw);
+    // Quads per workgroup: about 16 KiB of codes per workgroup, halved while fewer than 128
+    // workgroups would cover the chip, and at most about 2400 workgroups for the largest tables.
+    const int run = int(t->blocks) * (t->dtype == FG_Q4B32 ? 64 : 128);  // code bytes per quad
+    int qpw = std::max(1, 16384 / run);
+    while (qpw > 1 && (nq + qpw - 1) / qpw < 128) qpw /= 2;
+    qpw = std::min(16, std::max(qpw, (nq + 2399) / 2400));
     p.qpw = qpw;
+    p.qstride = 1;
     while (qpw > 1 && proj_smem(p, rows, in, out) > 64 * 1024) p.qpw = qpw = qpw / 2;
     const size_t smem = proj_smem(p, rows, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");

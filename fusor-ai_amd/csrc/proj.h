@@ -17,7 +17,10 @@ struct ProjParams {
     const int8_t *codes, *codes2;      // device table(s); codes2 is the SwiGLU up table
     const float *wscales, *wscales2;
     int B, G, K, n_rows;
-    int quad_begin, quad_end, qpw;
+    // Workgroup w owns quads base + j·qstride, j < qpw, base = quad_begin + (w / qstride)·qstride·qpw
+    // + w % qstride: consecutive quads when qstride is 1; the two halves of a rotary pair (quads
+    // D/8 apart) when the QKV epilogue asks for qstride = D/8, qpw = 2.
+    int quad_begin, quad_end, qpw, qstride;
     // input
     const float *x;
     const int8_t *q;
@@ -42,11 +45,8 @@ struct ProjParams {
     float *kcache, *vcache;
     size_t layer_base;
     int capacity, position;
-    // SwiGLU epilogue: the down projection's quantized input
-    int8_t *q_out;
-    float *s_out;
-    int32_t *c_out;
-    int zp_out;
+    // SwiGLU epilogue: silu(gate)·up, f32 (the down projection quantizes it in its prologue)
+    float *act_out;
 };
 
 // Byte offsets of the LDS regions (every region 16-byte aligned).
@@ -59,15 +59,15 @@ __host__ __device__ inline int align16(int b) { return (b + 15) & ~15; }
 __host__ __device__ inline ProjLayout proj_layout(int R, int K, int G, int NW, int in, int out)
 {
     const int NT = out == OUT_SWIGLU ? 2 : 1;
-    const int ny = out == OUT_SWIGLU ? 3 : 1;
+    const int ny = out == OUT_SWIGLU ? 2 : 1;
     ProjLayout l;
     l.off_s = align16(R * K);
     l.off_c = l.off_s + align16(R * G * 4);
     l.off_red = l.off_c + align16(R * G * 4);
     l.off_y = l.off_red + 16 * 4;
     l.off_terms = l.off_y + align16(ny * R * NW * 4);
-    l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * G * NW * 4));
-    l.total = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);
+    l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * NW * ((G + 3) & ~3) * 4));
+    l.total = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);  // the exact RMSNorm's row
     return l;
 }
 

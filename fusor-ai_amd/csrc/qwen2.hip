@@ -31,6 +31,7 @@ constexpr int kAttnThreads = 256;
 constexpr int kScoreKeys = 32;   // keys per workgroup of the scores
 constexpr int kWeighKeys = 256;  // keys per staged chunk of values
 constexpr int kWeighDims = 32;   // value dimensions per workgroup (one quantization group)
+constexpr int kHeadQuads = 16;  // quads per workgroup of the logits product
 
 struct AttnParams {
     const float *qkv;  // rotated query heads first
@@ -239,16 +240,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
             x[e] = v;
         }
         float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-        amax = fmaxf(0.0f, amax);
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        amax = max8(fmaxf(0.0f, amax));
         const float d = group_scale(amax, 127.0f);
         const int l0 = quantize_level(x[0], d), l1 = quantize_level(x[1], d), l2 = quantize_level(x[2], d), l3 = quantize_level(x[3], d);
-        int sum = l0 + l1 + l2 + l3;
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);
-        sum += __shfl_xor(sum, 4, 64);
+        const int sum = sum8(l0 + l1 + l2 + l3);
         const int G = (head * D + d0) / 32;
         reinterpret_cast<int *>(a.q)[G * 8 + sub] = pack4(l0, l1, l2, l3);
         if (sub == 0) {
@@ -313,6 +308,7 @@ struct fg_qwen2 {
     float *kcache, *vcache;
     // activations
     float *hidden, *qkv, *logits, *rope;  // rope: [capacity][cos | sin]
+    float *ffn;                           // silu(gate)·up, [ffn]
     int8_t *xq;
     float *xs;
     int32_t *xc;
@@ -345,7 +341,8 @@ int qkv_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(ly.qkv);
-    p.qpw = int(sh.head_dim / 4);  // one head per workgroup
+    p.qpw = 2;  // a rotary pair of quads per workgroup
+    p.qstride = int(sh.head_dim / 8);
     p.x = m->hidden;
     p.norm_w = ly.norm1;
     p.eps = sh.eps;
@@ -364,37 +361,39 @@ int qkv_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position
     return launch_proj(p, sh.dtype, IN_NORM, OUT_QKV, sh.exact != 0, st);
 }
 
-// 3. and 5. a projection of the prepared input added to the residual row.
-int residual_launch(fg_qwen2 *m, const fg_table *t, hipStream_t st)
+// 3. and 5. a projection added to the residual row: of the attention's quantized output (o), or
+// of the f32 silu(gate)·up row, quantized in the prologue (down).
+int residual_launch(fg_qwen2 *m, const fg_table *t, bool f32_input, hipStream_t st)
 {
     ProjParams p = table_params(t);
     p.qpw = 1;
-    p.q = m->xq;
-    p.as = m->xs;
-    p.corr = m->xc;
+    if (f32_input) {
+        p.x = m->ffn;
+    } else {
+        p.q = m->xq;
+        p.as = m->xs;
+        p.corr = m->xc;
+    }
     p.zp = m->zp;
     p.out = m->hidden;
     p.ld_out = long(t->quads * 4);
     p.accumulate = 1;
-    return launch_proj(p, m->shape.dtype, IN_PREQ, OUT_STORE, false, st);
+    return launch_proj(p, m->shape.dtype, f32_input ? IN_F32 : IN_PREQ, OUT_STORE, false, st);
 }
 
-// 4. RMSNorm -> gate and up -> silu(gate)·up quantized for down.
+// 4. RMSNorm -> gate and up -> silu(gate)·up.
 int swiglu_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, hipStream_t st)
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(ly.gate);
     p.codes2 = ly.up->codes;
     p.wscales2 = ly.up->scales;
-    p.qpw = 8;  // 32 outputs: one group of the down projection's input
+    p.qpw = 2;
     p.x = m->hidden;
     p.norm_w = ly.norm2;
     p.eps = sh.eps;
     p.zp = m->zp;
-    p.q_out = m->xq;
-    p.s_out = m->xs;
-    p.c_out = m->xc;
-    p.zp_out = m->zp;
+    p.act_out = m->ffn;
     return launch_proj(p, sh.dtype, IN_NORM, OUT_SWIGLU, sh.exact != 0, st);
 }
 
@@ -432,16 +431,16 @@ int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     int rc;
     if ((rc = qkv_launch(m, ly, li, position, st))) return rc;
     if ((rc = attention_launch(m, li, position, st))) return rc;
-    if ((rc = residual_launch(m, ly.o, st))) return rc;
+    if ((rc = residual_launch(m, ly.o, false, st))) return rc;
     if ((rc = swiglu_launch(m, ly, st))) return rc;
-    return residual_launch(m, ly.down, st);
+    return residual_launch(m, ly.down, true, st);
 }
 
 int head_launch(fg_qwen2 *m, hipStream_t st)
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(m->table);
-    p.qpw = 64;
+    p.qpw = kHeadQuads;
     p.x = m->hidden;
     p.norm_w = m->final_norm;
     p.eps = sh.eps;
@@ -472,17 +471,20 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
         return set_error(FG_ERR_SHAPE, "fg_qwen2_create: heads must be a multiple of kv_heads");
     if (sh.head_dim != 32 && sh.head_dim != 64 && sh.head_dim != 128)
         return set_error(FG_ERR_SHAPE, "fg_qwen2_create: head_dim must be 32, 64 or 128");
-    if (sh.hidden % 32 || sh.ffn % 32 || sh.hidden > 16384 || sh.capacity == 0 || sh.capacity > 8192)
-        return set_error(FG_ERR_SHAPE, "fg_qwen2_create: hidden and ffn must be whole groups (hidden <= 16384, capacity <= 8192)");
+    if (sh.hidden % 32 || sh.ffn % 32 || sh.hidden > 4096 || sh.capacity == 0 || sh.capacity > 8192)
+        return set_error(FG_ERR_SHAPE, "fg_qwen2_create: hidden and ffn must be whole groups (hidden <= 4096, capacity <= 8192)");
     const size_t qkv_w = (sh.heads + 2 * sh.kv_heads) * sh.head_dim, width = sh.heads * sh.head_dim;
     for (size_t l = 0; l < sh.layers; l++) {
         const fg_qwen2_layer &ly = layers[l];
-        if (!ly.norm1 || !ly.norm2 || !table_is(ly.qkv, sh.dtype, qkv_w, sh.hidden) || !table_is(ly.o, sh.dtype, sh.hidden, width) ||
+        if (!ly.norm1 || !ly.norm2 || (reinterpret_cast<uintptr_t>(ly.norm1) & 15) || (reinterpret_cast<uintptr_t>(ly.norm2) & 15))
+            return set_error(FG_ERR_ARG, "fg_qwen2_create: norm weights must be 16-byte aligned device arrays");
+        if (!table_is(ly.qkv, sh.dtype, qkv_w, sh.hidden) || !table_is(ly.o, sh.dtype, sh.hidden, width) ||
             !table_is(ly.gate, sh.dtype, sh.ffn, sh.hidden) || !table_is(ly.up, sh.dtype, sh.ffn, sh.hidden) ||
             !table_is(ly.down, sh.dtype, sh.hidden, sh.ffn))
             return set_error(FG_ERR_SHAPE, "fg_qwen2_create: layer " + std::to_string(l) + " tables do not fit the shape");
     }
     if (!table_is(table, sh.dtype, sh.vocab, sh.hidden)) return set_error(FG_ERR_SHAPE, "fg_qwen2_create: the table is not [vocab, hidden]");
+    if (reinterpret_cast<uintptr_t>(final_norm) & 15) return set_error(FG_ERR_ARG, "fg_qwen2_create: norm weights must be 16-byte aligned device arrays");
     fg_qwen2 *m = new fg_qwen2();
     m->shape = sh;
     m->layers.assign(layers, layers + sh.layers);
@@ -491,7 +493,7 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
     m->kcache = kcache;
     m->vcache = vcache;
     m->zp = zero_point_of(sh.dtype);
-    m->head_groups = int((table->quads + 63) / 64);
+    m->head_groups = int((table->quads + kHeadQuads - 1) / kHeadQuads);
     // attention LDS: a block of keys and the group's queries; a chunk of values and the weights
     const int D = int(sh.head_dim);
     const int group = int(sh.heads / sh.kv_heads);
@@ -509,6 +511,7 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
     } allocs[] = {
         {reinterpret_cast<void **>(&m->hidden), sh.hidden * 4},
         {reinterpret_cast<void **>(&m->qkv), (qkv_w + 3) / 4 * 4 * 4},
+        {reinterpret_cast<void **>(&m->ffn), sh.ffn * 4},
         {reinterpret_cast<void **>(&m->logits), padded_vocab * 4},
         {reinterpret_cast<void **>(&m->rope), sh.capacity * sh.head_dim * 4},
         {reinterpret_cast<void **>(&m->xq), widest},
@@ -589,7 +592,7 @@ extern "C" int fg_qwen2_step(fg_qwen2 *m, int token, size_t position, float *hid
 extern "C" int fg_qwen2_free(fg_qwen2 *m)
 {
     if (!m) return FG_OK;
-    void *ptrs[] = {m->hidden, m->qkv, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores};
+    void *ptrs[] = {m->hidden, m->qkv, m->ffn, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete m;

@@ -190,12 +190,12 @@ __global__ void quantize_rows_kernel(const float *__restrict__ x, size_t groups,
     bool active = g < groups;
     float4 v = active ? reinterpret_cast<const float4 *>(x)[g * LANES + sub] : make_float4(0, 0, 0, 0);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(0.0f, amax);
-    for (int m = 1; m < LANES; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+    amax = max8(fmaxf(0.0f, amax));
+    for (int m = 8; m < LANES; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
     float d = group_scale(amax, 127.0f);
     int l0 = quantize_level(v.x, d), l1 = quantize_level(v.y, d), l2 = quantize_level(v.z, d), l3 = quantize_level(v.w, d);
-    int sum = l0 + l1 + l2 + l3;
-    for (int m = 1; m < LANES; m <<= 1) sum += __shfl_xor(sum, m, 64);
+    int sum = sum8(l0 + l1 + l2 + l3);
+    for (int m = 8; m < LANES; m <<= 1) sum += __shfl_xor(sum, m, 64);
     if (!active) return;
     reinterpret_cast<int *>(q)[g * LANES + sub] = pack4(l0, l1, l2, l3);
     if (sub == 0) {

@@ -72,6 +72,8 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 
 // ------------------------------------------------------------------ device helpers
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ int dot4(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
 
 // The partner lane's value in pairs (lane ^ 1), through DPP.
@@ -93,6 +95,16 @@ __device__ __forceinline__ int sum8(int v)
     v += xor1(v);
     v += xor2(v);
     return v + mirror8(v);
+}
+// Maximum over the wave (NaN ignored, as fmaxf does): groups of 8 through DPP, then the eight
+// group results read out.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = max8(v);
+    float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+#pragma unroll
+    for (int g = 8; g < 64; g += 8) m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), g)));
+    return m;
 }
 // Sum over the wave, in no particular order: groups of 8 through DPP, then the eight group
 // results read out and added.

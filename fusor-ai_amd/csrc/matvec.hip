@@ -36,8 +36,6 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ int dot16(int4 w, int4 a) { return dot4(w.w, a.w, dot4(w.z, a.z, dot4(w.y, a.y, dot4(w.x, a.x, 0)))); }
 
-typedef float v4f __attribute__((ext_vector_type(4)));
-
 // Σ t[g] for g in 0..n, added in index order from +0. `t` is 16-byte aligned and readable up to n
 // rounded up to 4. Whole runs of 32 terms come in eight 128-bit reads, the next run in flight
 // while the current one is added (straight-line adds, no per-term branch); then the tail.
@@ -94,6 +92,8 @@ struct StageRegs {
     int c0, c1, c2, c3;
     v4f f0, f1, f2, f3;  // f32 rows (IN_F32) or the row to normalize (IN_NORM)
     v4f f4, f5, f6, f7;  // more f32 rows (IN_F32)
+    v4f pa[kMaxChunks];  // IN_ATTN: this lane's four sums of every chunk, and the chunks' max and total
+    float pm[kMaxChunks], pl[kMaxChunks];
     v4f w0, w1, w2, w3;  // the RMSNorm weight (IN_NORM)
 };
 
@@ -129,6 +129,17 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
         g.f5 = x4[min(tid + 5 * kThreads, n4 - 1)];
         g.f6 = x4[min(tid + 6 * kThreads, n4 - 1)];
         g.f7 = x4[min(tid + 7 * kThreads, n4 - 1)];
+    } else if (IN == IN_ATTN) {
+        // lane t merges float4 t of the attention row (head t·4 / D); every chunk's record at once
+        const int e = min(tid, K / 4 - 1);
+        const int h = e * 4 / p.D, d4 = e * 4 - h * p.D;
+#pragma unroll
+        for (int c = 0; c < kMaxChunks; c++) {
+            const float *rec = p.part + size_t(h * p.chunks + min(c, p.chunks - 1)) * (p.D + 4);
+            g.pm[c] = rec[0];
+            g.pl[c] = rec[1];
+            g.pa[c] = *reinterpret_cast<const v4f *>(rec + 4 + d4);
+        }
     } else {
         // one row of at most 4 · 256 float4s (K <= 4096, checked on the host)
         const v4f *x4 = reinterpret_cast<const v4f *>(p.x);
@@ -207,6 +218,24 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
 #undef FG_Q8
         for (int i = tid + 8 * kThreads; i < n4; i += kThreads)
             quantize8(reinterpret_cast<const v4f *>(p.x)[i], p.zp, i / 8, act_q, act_s, act_c);
+    } else if (IN == IN_ATTN) {
+        // the chunks' softmax states merged (flash decoding): M = max m_c, L = Σ l_c·e^(m_c − M),
+        // out = Σ acc_c·e^(m_c − M) / L; then the row quantized (8 lanes per group of 32)
+        float M = g.pm[0];
+#pragma unroll
+        for (int c = 1; c < kMaxChunks; c++)
+            if (c < p.chunks) M = fmaxf(M, g.pm[c]);
+        float L = 0.0f;
+        v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < kMaxChunks; c++) {
+            if (c < p.chunks) {
+                const float e = ref_exp(g.pm[c] - M);
+                L = L + g.pl[c] * e;
+                o = o + g.pa[c] * e;
+            }
+        }
+        if (tid < K / 4) quantize8(o / L, p.zp, tid / 8, act_q, act_s, act_c);
     } else {
         // rms_norm (ops.rs:7-16): mean of squares, 1/sqrt(mean + eps), x·inverse·weight; then the
         // quantization of the normed row. Thread t holds float4s t, t + 256, ... of the row, so
@@ -553,6 +582,8 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     if (out == OUT_QKV && (p.qpw != 2 || p.qstride * 8 != p.D))
         return set_error(FG_ERR_SHAPE, "the QKV epilogue takes one rotary pair per workgroup");
     if (in == IN_NORM && p.K > 4 * 4 * kThreads) return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
+    if (in == IN_ATTN && (p.K > 4 * kThreads || p.chunks < 1 || p.chunks > kMaxChunks || p.heads * p.D != p.K))
+        return set_error(FG_ERR_SHAPE, "the attention merge takes rows of at most 1024 and 1 to 8 chunks");
     const unsigned grid = p.qstride == 1 ? unsigned((nq + p.qpw - 1) / p.qpw) : unsigned(nq / span * p.qstride);
     const size_t smem = proj_smem(p, 1, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
@@ -571,6 +602,9 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
         if (in == IN_F32)
             return q4 ? launch_one<4, 1, IN_F32, OUT_STORE, false, 8>(p, smem, grid, s)
                       : launch_one<8, 1, IN_F32, OUT_STORE, false, 8>(p, smem, grid, s);
+        if (in == IN_ATTN)
+            return q4 ? launch_one<4, 1, IN_ATTN, OUT_STORE, false, 8>(p, smem, grid, s)
+                      : launch_one<8, 1, IN_ATTN, OUT_STORE, false, 8>(p, smem, grid, s);
         return q4 ? launch_one<4, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s)
                   : launch_one<8, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s);
     }

@@ -6,9 +6,12 @@
 
 namespace fg {
 
-// Input of a projection: rows already quantized, f32 rows quantized in-kernel, or one f32 row
-// RMS-normalized then quantized in-kernel (rms_norm, ops.rs:7-16).
-constexpr int IN_PREQ = 0, IN_F32 = 1, IN_NORM = 2;
+// Input of a projection: rows already quantized, f32 rows quantized in-kernel, one f32 row
+// RMS-normalized then quantized in-kernel (rms_norm, ops.rs:7-16), or the attention's output row
+// merged from per-chunk softmax states, then quantized.
+constexpr int IN_PREQ = 0, IN_F32 = 1, IN_NORM = 2, IN_ATTN = 3;
+// Chunks of keys per query head in the fast attention; the output projection merges them.
+constexpr int kMaxChunks = 8;
 // Output: store (bias / residual / greedy candidates), the int32 group accumulators, the QKV
 // epilogue, the gated feed-forward epilogue.
 constexpr int OUT_STORE = 0, OUT_DOTS = 1, OUT_QKV = 2, OUT_SWIGLU = 3;
@@ -29,6 +32,8 @@ struct ProjParams {
     int zp;
     const float *norm_w;
     float eps;
+    const float *part;  // IN_ATTN: per (head, chunk) records of D + 4 floats: max, total, -, -, sums
+    int chunks;
     // store
     const float *bias;
     float *out;

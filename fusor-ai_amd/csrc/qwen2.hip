@@ -32,6 +32,7 @@ constexpr int kScoreKeys = 32;   // keys per workgroup of the scores
 constexpr int kWeighKeys = 256;  // keys per staged chunk of values
 constexpr int kWeighDims = 32;   // value dimensions per workgroup (one quantization group)
 constexpr int kHeadQuads = 16;  // quads per workgroup of the logits product
+constexpr int kTileKeys = 64;   // keys per tile of the fast attention
 
 struct AttnParams {
     const float *qkv;  // rotated query heads first
@@ -39,6 +40,8 @@ struct AttnParams {
     size_t layer_base;
     int heads, kv_heads, D, capacity, keys;
     float *scores;  // [heads][capacity]
+    float *part;    // fast attention: [heads][chunks][D + 4]
+    int chunks, per_chunk;
     int zp;
     int8_t *q;
     float *scales;
@@ -253,6 +256,89 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
     }
 }
 
+// The fast (parallel-order) attention, first half: the softmax state of one query head over one
+// chunk of keys (flash decoding). Per tile of kTileKeys keys: the scores q·k_j·(1/√D) (ops.rs:310-
+// 326; four lanes per key), the running maximum m, e^(s_j − m) through ops::exp, the running total
+// l and the running weighted sum of values (ops.rs:329-342), both rescaled by e^(m_old − m) when
+// the maximum moves. Writes (m, l, −, −, acc[D]) per (head, chunk); the output projection's
+// prologue merges the chunks. Grid: (heads, chunks).
+template <int D>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnParams a)
+{
+    __shared__ float pw[kTileKeys];
+    __shared__ float red[8];
+    __shared__ float sums[kAttnThreads];
+    constexpr int DQ = D / 4;             // dims of a key per lane
+    constexpr int KG = kAttnThreads / D;  // key groups of the weighted sum
+    constexpr int VK = kTileKeys / KG;    // values per lane per tile
+    const int head = blockIdx.x, c = blockIdx.y;
+    const int kv = head / (a.heads / a.kv_heads);
+    const int first = c * a.per_chunk, last = min(a.keys, first + a.per_chunk);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int jk = tid >> 2, part = tid & 3;  // scores: key jk of the tile, dims part·DQ ..
+    const int d = tid % D, g = tid / D;       // weighted sum: dim d over keys g, g + KG, ..
+    const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
+    const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D;
+    v4f q[DQ / 4];
+#pragma unroll
+    for (int i = 0; i < DQ / 4; i++) q[i] = *reinterpret_cast<const v4f *>(a.qkv + size_t(head) * D + part * DQ + 4 * i);
+    const float scale = 1.0f / sqrtf(float(D));
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int j0 = first; j0 < last; j0 += kTileKeys) {
+        const int n = min(kTileKeys, last - j0);
+        // every load of the tile first (branch-free: keys past n re-read key j0)
+        v4f k[DQ / 4];
+        const float *krow = kbase + size_t((j0 + (jk < n ? jk : 0)) % a.capacity) * D + part * DQ;
+#pragma unroll
+        for (int i = 0; i < DQ / 4; i++) k[i] = *reinterpret_cast<const v4f *>(krow + 4 * i);
+        float v[VK];
+#pragma unroll
+        for (int e = 0; e < VK; e++) {
+            const int j = g + e * KG;
+            v[e] = vbase[size_t((j0 + (j < n ? j : 0)) % a.capacity) * D + d];
+        }
+        v4f sv = q[0] * k[0];
+#pragma unroll
+        for (int i = 1; i < DQ / 4; i++) sv = sv + q[i] * k[i];
+        float s = (sv.x + sv.y) + (sv.z + sv.w);
+        s = s + __int_as_float(xor1(__float_as_int(s)));
+        s = s + __int_as_float(xor2(__float_as_int(s)));
+        s = jk < n ? s * scale : -INFINITY;
+        const float wm = wave_max(s);
+        if (lane == 0) red[wave] = wm;
+        __syncthreads();
+        const float m_new = fmaxf(m, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        const float r = m == -INFINITY ? 0.0f : ref_exp(m - m_new);
+        const float pj = jk < n ? ref_exp(s - m_new) : 0.0f;
+        const float ws = wave_sum_unordered(part == 0 ? pj : 0.0f);
+        if (part == 0) pw[jk] = pj;
+        if (lane == 0) red[4 + wave] = ws;
+        __syncthreads();
+        l = l * r + ((red[4] + red[5]) + (red[6] + red[7]));
+        m = m_new;
+        acc = acc * r;
+#pragma unroll
+        for (int e = 0; e < VK; e++) {
+            const int j = g + e * KG;
+            acc = acc + (j < n ? pw[j] * v[e] : 0.0f);
+        }
+        __syncthreads();  // pw and red are the next tile's
+    }
+    sums[tid] = acc;
+    __syncthreads();
+    float *rec = a.part + size_t(head * a.chunks + c) * (D + 4);
+    if (g == 0) {
+        float o = acc;
+#pragma unroll
+        for (int gg = 1; gg < KG; gg++) o = o + sums[gg * D + d];
+        rec[4 + d] = o;
+    }
+    if (tid == 0) {
+        rec[0] = m;
+        rec[1] = l;
+    }
+}
+
 // Prediction::greedy (lm.rs:169-179) over the head's per-workgroup candidates: the first index of
 // the largest logit; NaNs never win, and a NaN first logit keeps index 0.
 __global__ __launch_bounds__(1024) void greedy_kernel(const float *__restrict__ pval, const int32_t *__restrict__ pidx, int n,
@@ -316,6 +402,8 @@ struct fg_qwen2 {
     int32_t *pidx;
     int head_groups;  // workgroups of the head product (greedy candidates)
     float *scores;     // [heads][capacity]
+    float *part;       // fast attention: [heads][chunks][D + 4]
+    int chunks, per_chunk;
     size_t score_smem, weigh_smem;
     int zp;
 };
@@ -361,14 +449,23 @@ int qkv_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position
     return launch_proj(p, sh.dtype, IN_NORM, OUT_QKV, sh.exact != 0, st);
 }
 
-// 3. and 5. a projection added to the residual row: of the attention's quantized output (o), or
-// of the f32 silu(gate)·up row, quantized in the prologue (down).
-int residual_launch(fg_qwen2 *m, const fg_table *t, bool f32_input, hipStream_t st)
+// Whether the attention runs as flash decoding merged by the output projection (parallel order).
+bool fast_attention(const fg_qwen2 *m) { return !m->shape.exact && m->shape.heads * m->shape.head_dim <= 1024; }
+
+// 3. and 5. a projection added to the residual row: of the attention's output (o: quantized by
+// the attention, or merged from its chunks and quantized in the prologue), or of the f32
+// silu(gate)·up row, quantized in the prologue (down).
+int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st)
 {
     ProjParams p = table_params(t);
     p.qpw = 1;
-    if (f32_input) {
+    if (in == IN_F32) {
         p.x = m->ffn;
+    } else if (in == IN_ATTN) {
+        p.part = m->part;
+        p.chunks = m->chunks;
+        p.heads = int(m->shape.heads);
+        p.D = int(m->shape.head_dim);
     } else {
         p.q = m->xq;
         p.as = m->xs;
@@ -378,7 +475,7 @@ int residual_launch(fg_qwen2 *m, const fg_table *t, bool f32_input, hipStream_t 
     p.out = m->hidden;
     p.ld_out = long(t->quads * 4);
     p.accumulate = 1;
-    return launch_proj(p, m->shape.dtype, f32_input ? IN_F32 : IN_PREQ, OUT_STORE, false, st);
+    return launch_proj(p, m->shape.dtype, in, OUT_STORE, false, st);
 }
 
 // 4. RMSNorm -> gate and up -> silu(gate)·up.
@@ -415,6 +512,23 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     a.q = m->xq;
     a.scales = m->xs;
     a.corr = m->xc;
+    if (fast_attention(m)) {
+        // chunks of whole tiles, at most kMaxChunks per head
+        const int per = (a.keys + kMaxChunks - 1) / kMaxChunks;
+        m->per_chunk = std::max(kTileKeys, (per + kTileKeys - 1) / kTileKeys * kTileKeys);
+        m->chunks = (a.keys + m->per_chunk - 1) / m->per_chunk;
+        a.part = m->part;
+        a.chunks = m->chunks;
+        a.per_chunk = m->per_chunk;
+        const dim3 grid(unsigned(sh.heads), unsigned(m->chunks));
+        switch (sh.head_dim) {
+        case 32: attn_partial_kernel<32><<<grid, kAttnThreads, 0, st>>>(a); break;
+        case 64: attn_partial_kernel<64><<<grid, kAttnThreads, 0, st>>>(a); break;
+        default: attn_partial_kernel<128><<<grid, kAttnThreads, 0, st>>>(a); break;
+        }
+        FG_HIP(hipGetLastError());
+        return FG_OK;
+    }
     const dim3 sgrid(unsigned(sh.kv_heads), unsigned((a.keys + kScoreKeys - 1) / kScoreKeys));
     attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
     FG_HIP(hipGetLastError());
@@ -431,9 +545,9 @@ int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     int rc;
     if ((rc = qkv_launch(m, ly, li, position, st))) return rc;
     if ((rc = attention_launch(m, li, position, st))) return rc;
-    if ((rc = residual_launch(m, ly.o, false, st))) return rc;
+    if ((rc = residual_launch(m, ly.o, fast_attention(m) ? IN_ATTN : IN_PREQ, st))) return rc;
     if ((rc = swiglu_launch(m, ly, st))) return rc;
-    return residual_launch(m, ly.down, true, st);
+    return residual_launch(m, ly.down, IN_F32, st);
 }
 
 int head_launch(fg_qwen2 *m, hipStream_t st)
@@ -520,6 +634,7 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
         {reinterpret_cast<void **>(&m->pval), size_t(m->head_groups) * 4},
         {reinterpret_cast<void **>(&m->pidx), size_t(m->head_groups) * 4},
         {reinterpret_cast<void **>(&m->scores), sh.heads * sh.capacity * 4},
+        {reinterpret_cast<void **>(&m->part), sh.heads * kMaxChunks * (sh.head_dim + 4) * 4},
     };
     for (auto &a : allocs) {
         hipError_t e = hipMalloc(a.ptr, a.bytes);
@@ -592,7 +707,7 @@ extern "C" int fg_qwen2_step(fg_qwen2 *m, int token, size_t position, float *hid
 extern "C" int fg_qwen2_free(fg_qwen2 *m)
 {
     if (!m) return FG_OK;
-    void *ptrs[] = {m->hidden, m->qkv, m->ffn, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores};
+    void *ptrs[] = {m->hidden, m->qkv, m->ffn, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores, m->part};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete m;

@@ -290,7 +290,9 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
 }
 
 // FMT: 8 for signed 8-bit levels (Q7b32 folded, Q8b32), 4 for offset nibbles (Q4b32).
-template <int FMT, int R, int IN, int OUT, bool EXACT, int kBatch>
+// TREE: each output's group terms summed by a team of lanes and a lane reduction instead of in
+// group order (the decoder's parallel-order mode; the product's own entry points never use it).
+template <int FMT, int R, int IN, int OUT, bool EXACT, int kBatch, bool TREE>
 __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -401,11 +403,18 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     float sa[kBatch], sb[kBatch];
     StageRegs g;
     stage_issue<R, IN>(p, g);
+    // Who sums which output: one thread per output, or (TREE) a team of `team` lanes per output.
+    const int outs = NT * R * NW;
+    int team = 1;
+    if (TREE)
+        while (team < 64 && outs * team * 2 <= kThreads) team <<= 1;
+    const int my_out = TREE ? int(threadIdx.x) / team : int(threadIdx.x);
+    const int sub = int(threadIdx.x) - my_out * team;
     // the residual row this workgroup adds to, read early (linear.rs:139-142); read whether or not
     // it is added, so that no branch splits the loads before the weights' first batch
     float resid = 0.0f;
     if (OUT == OUT_STORE) {
-        const int r = int(threadIdx.x) / NW, nl = int(threadIdx.x) - r * NW;
+        const int r = my_out / NW, nl = my_out - r * NW;
         const bool mine = r < R && nl < nq * 4;
         resid = p.out[mine ? r * p.ld_out + (output_of(nl) - p.col_begin) : 0];
     }
@@ -427,12 +436,10 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     if (OUT == OUT_DOTS) return;
     __syncthreads();
 
-    // Group order: the reference's sequential sum, one thread per (table, row, output).
-    for (int i = threadIdx.x; i < NT * R * NW; i += kThreads) {
+    // Output i of (table, row, column): bias, then stored (written or added to the residual row).
+    auto finish = [&](int i, float s) {
         const int tb = i / (R * NW), rem = i - tb * R * NW;
         const int r = rem / NW, nl = rem - r * NW;
-        if (nl >= nq * 4) continue;
-        float s = ordered_sum(terms + ((tb * R + r) * NW + nl) * Gp, G);
         const int n = output_of(nl);
         if (OUT != OUT_SWIGLU && p.bias && n < p.n_rows) s = s + p.bias[n];
         if (OUT == OUT_STORE) {
@@ -442,6 +449,24 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             *o = p.accumulate ? prior + s : s;
         }
         ybuf[i] = s;
+    };
+    auto live = [&](int i) { return i < outs && (i % NW) < nq * 4; };
+    if (TREE) {
+        // strided partial sums, then the team's lanes reduced (lanes of one wave)
+        float s = 0.0f;
+        if (live(my_out)) {
+            const float *t = terms + my_out * Gp;  // [tb][r][nl] rows in output order
+            for (int g = sub; g < G; g += team) s = s + t[g];
+        }
+        if (team >= 2) s = s + __int_as_float(xor1(__float_as_int(s)));
+        if (team >= 4) s = s + __int_as_float(xor2(__float_as_int(s)));
+        if (team >= 8) s = s + __int_as_float(mirror8(__float_as_int(s)));
+        for (int m = 8; m < team; m <<= 1) s = s + __shfl_xor(s, m, 64);
+        if (sub == 0 && live(my_out)) finish(my_out, s);
+    } else {
+        // group order: the reference's sequential sum, one thread per (table, row, output)
+        for (int i = threadIdx.x; i < outs; i += kThreads)
+            if (live(i)) finish(i, ordered_sum(terms + i * Gp, G));
     }
 
     if (OUT == OUT_STORE) {
@@ -520,10 +545,10 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     }
 }
 
-template <int FMT, int R, int IN, int OUT, bool EXACT, int NB = 8>
+template <int FMT, int R, int IN, int OUT, bool EXACT, int NB = 8, bool TREE = false>
 int launch_one(const ProjParams &p, size_t smem, unsigned grid, hipStream_t s)
 {
-    auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT, NB>;
+    auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT, NB, TREE>;
     if (smem > 64 * 1024) {
         static bool raised = false;
         if (!raised) {
@@ -561,7 +586,8 @@ int dispatch_rows(const ProjParams &p, int rows, int in, bool dots, size_t smem,
 template <int FMT, int IN, int OUT, int NB>
 int dispatch_exact(const ProjParams &p, bool exact, size_t smem, unsigned grid, hipStream_t s)
 {
-    return exact ? launch_one<FMT, 1, IN, OUT, true, NB>(p, smem, grid, s) : launch_one<FMT, 1, IN, OUT, false, NB>(p, smem, grid, s);
+    return exact ? launch_one<FMT, 1, IN, OUT, true, NB, false>(p, smem, grid, s)
+                 : launch_one<FMT, 1, IN, OUT, false, NB, true>(p, smem, grid, s);
 }
 
 }  // namespace
@@ -600,13 +626,13 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
             return q4 ? dispatch_exact<4, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s)
                       : dispatch_exact<8, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s);
         if (in == IN_F32)
-            return q4 ? launch_one<4, 1, IN_F32, OUT_STORE, false, 8>(p, smem, grid, s)
-                      : launch_one<8, 1, IN_F32, OUT_STORE, false, 8>(p, smem, grid, s);
-        if (in == IN_ATTN)
-            return q4 ? launch_one<4, 1, IN_ATTN, OUT_STORE, false, 8>(p, smem, grid, s)
-                      : launch_one<8, 1, IN_ATTN, OUT_STORE, false, 8>(p, smem, grid, s);
-        return q4 ? launch_one<4, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s)
-                  : launch_one<8, 1, IN_PREQ, OUT_STORE, false, 8>(p, smem, grid, s);
+            return q4 ? dispatch_exact<4, IN_F32, OUT_STORE, 8>(p, exact, smem, grid, s)
+                      : dispatch_exact<8, IN_F32, OUT_STORE, 8>(p, exact, smem, grid, s);
+        if (in == IN_ATTN)  // the merge is the parallel-order attention's
+            return q4 ? launch_one<4, 1, IN_ATTN, OUT_STORE, false, 8, true>(p, smem, grid, s)
+                      : launch_one<8, 1, IN_ATTN, OUT_STORE, false, 8, true>(p, smem, grid, s);
+        return q4 ? dispatch_exact<4, IN_PREQ, OUT_STORE, 8>(p, exact, smem, grid, s)
+                  : dispatch_exact<8, IN_PREQ, OUT_STORE, 8>(p, exact, smem, grid, s);
     }
 }
 

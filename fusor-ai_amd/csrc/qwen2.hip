@@ -475,7 +475,7 @@ int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st)
     p.out = m->hidden;
     p.ld_out = long(t->quads * 4);
     p.accumulate = 1;
-    return launch_proj(p, m->shape.dtype, in, OUT_STORE, false, st);
+    return launch_proj(p, m->shape.dtype, in, OUT_STORE, m->shape.exact != 0, st);
 }
 
 // 4. RMSNorm -> gate and up -> silu(gate)·up.

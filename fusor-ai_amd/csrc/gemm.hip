@@ -9,8 +9,8 @@
 // levels over K = 32, exactly one block: its int32 results are the group accumulators D_g of a
 // 32x32 output tile, exact. Weight levels are signed on the device (Q7b32 stored as u - 64; Q4b32
 // nibbles widened to u - 8 in registers), so no correction term is needed. Each wave owns a 32 x
-// 64 output tile (two MFMAs per block) and keeps the running f32 sums in registers; the K loop
-// walks the blocks in order, so the sums are the reference's to the bit.
+// 32 or 32 x 64 output tile (one or two MFMAs per block) and keeps the running f32 sums in
+// registers; the K loop walks the blocks in order, so the sums are the reference's to the bit.
 //
 // MFMA operand layout (32x32xK): lane l feeds row (or column) l % 32 and K-half l / 32; the same
 // K positions are used for both operands, so the sum covers the block's 32 inputs. Result:
@@ -40,87 +40,143 @@ struct GemmParams {
     int dots_cols;
 };
 
-template <int FMT>
-__device__ __forceinline__ v4i load_weights(const GemmParams &p, int n, int b, int h, bool valid)
-{
-    if (!valid) return v4i{0, 0, 0, 0};
-    const int quad = n >> 2, L = n & 3;
-    if (FMT == 8) return *reinterpret_cast<const v4i *>(p.codes + (size_t(quad) * p.B + b) * 128 + L * 32 + h * 16);
-    v4i raw = *reinterpret_cast<const v4i *>(p.codes + (size_t(quad) * p.B + b) * 64 + L * 16);
-    const int sh = h * 4;
-    return v4i{nibbles_signed(raw.x >> sh), nibbles_signed(raw.y >> sh), nibbles_signed(raw.z >> sh),
-               nibbles_signed(raw.w >> sh)};
-}
+// One wave per workgroup and per 32 x 32·TN output tile (TN MFMAs per block): enough waves to
+// spread the exact rescale, four VALU operations per output per block and the product's bound,
+// over every SIMD. Operands stream straight from memory, kDepth blocks ahead of the block being
+// multiplied (a ring of registers); rows and columns past the edges re-read the last valid one.
+constexpr int kDepth = 4;
 
-// WM waves along M (a 32·WM-row tile), 4 / WM along N (64 columns each).
-template <int FMT, int WM, bool DOTS>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmParams p)
-{
-    constexpr int WN = 4 / WM;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave % WM, wn = wave / WM;
-    const int i = lane & 31, h = lane >> 5;
-    const int m0 = int(blockIdx.y) * 32 * WM + wm * 32;
-    const int n0 = p.col_begin + int(blockIdx.x) * 64 * WN + wn * 64;
-    if (m0 >= p.M || n0 >= p.col_end) return;
+template <int TN, bool LDS_SCALES>
+struct Stage {
+    v4i a;        // this lane's 16 activation levels
+    v4i w[TN];    // 16 weight levels (or 32 packed nibbles) of this lane's column in each sub-tile
+    float ws[TN]; // the weight scale of those columns
+    v4f s0, s1, s2, s3;  // activation scales of this lane's 16 rows (when not staged in LDS)
+};
 
-    const int row = m0 + i;
-    const bool row_ok = row < p.M;
-    const int n_a = n0 + i, n_b = n0 + 32 + i;
-    const bool ok_a = n_a < p.col_end, ok_b = n_b < p.col_end;
+// LDS_SCALES: the tile's activation scales for every block staged in LDS once (32 floats per
+// block), so that the ring of registers holds operands only (more waves per SIMD).
+template <int FMT, int TN, bool DOTS, bool LDS_SCALES>
+__global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
+{
+    extern __shared__ __align__(16) float tile_scales[];  // [B][32] when LDS_SCALES
+    constexpr int QB = FMT == 8 ? 128 : 64;  // device bytes per quad block
+    const int lane = threadIdx.x, i = lane & 31, h = lane >> 5;
+    const int m0 = int(blockIdx.y) * 32, n0 = p.col_begin + int(blockIdx.x) * 32 * TN;
+    const int row = min(m0 + i, p.M - 1);
     const int8_t *arow = p.q + size_t(row) * p.K + h * 16;
+    const float *asrow = p.as_t + m0 + 4 * h;
+    const int8_t *wrow[TN];
+    const float *wsrow[TN];
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        const int nc = min(n0 + 32 * t + i, p.col_end - 1);
+        wrow[t] = p.codes + size_t(nc >> 2) * p.B * QB + (nc & 3) * (QB / 4) + (FMT == 8 ? h * 16 : 0);
+        wsrow[t] = p.wscales + size_t(nc >> 2) * p.G * 4 + (nc & 3);
+    }
+    const int B = p.B;
+    if (LDS_SCALES) {
+        // rows m0 .. m0 + 31 of as_t for every block: 8 float4 per block
+        for (int e = lane; e < B * 8; e += 64) {
+            const int b = e >> 3, c = e & 7;
+            reinterpret_cast<v4f *>(tile_scales)[e] = *reinterpret_cast<const v4f *>(p.as_t + size_t(b) * p.Mpad + m0 + 4 * c);
+        }
+    }
 
-    float s0[16], s1[16];
+    auto fetch = [&](int b, Stage<TN, LDS_SCALES> &st) {
+        st.a = *reinterpret_cast<const v4i *>(arow + b * 32);
 #pragma unroll
-    for (int v = 0; v < 16; v++) s0[v] = s1[v] = 0.0f;
+        for (int t = 0; t < TN; t++) {
+            st.w[t] = *reinterpret_cast<const v4i *>(wrow[t] + size_t(b) * QB);
+            st.ws[t] = wsrow[t][size_t(b) * 4];
+        }
+        if (!LDS_SCALES) {
+            const float *ap = asrow + size_t(b) * p.Mpad;
+            st.s0 = *reinterpret_cast<const v4f *>(ap);
+            st.s1 = *reinterpret_cast<const v4f *>(ap + 8);
+            st.s2 = *reinterpret_cast<const v4f *>(ap + 16);
+            st.s3 = *reinterpret_cast<const v4f *>(ap + 24);
+        }
+    };
 
-    for (int b = 0; b < p.B; b++) {
-        const v4i a = row_ok ? *reinterpret_cast<const v4i *>(arow + b * 32) : v4i{0, 0, 0, 0};
-        const v4i wa = load_weights<FMT>(p, n_a, b, h, ok_a);
-        const v4i wb = load_weights<FMT>(p, n_b, b, h, ok_b);
-        const float ws_a = ok_a ? p.wscales[(size_t(n_a >> 2) * p.G + b) * 4 + (n_a & 3)] : 0.0f;
-        const float ws_b = ok_b ? p.wscales[(size_t(n_b >> 2) * p.G + b) * 4 + (n_b & 3)] : 0.0f;
-        const float *asb = p.as_t + size_t(b) * p.Mpad + m0 + 4 * h;
-        float4 as4[4];
+    float acc[TN][16];
 #pragma unroll
-        for (int u = 0; u < 4; u++) as4[u] = *reinterpret_cast<const float4 *>(asb + 8 * u);
-        const v16i zero = {0};
-        const v16i da = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, wa, zero, 0, 0, 0);
-        const v16i db = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, wb, zero, 0, 0, 0);
-        if (DOTS) {
+    for (int t = 0; t < TN; t++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (r < p.M) {
-                    if (ok_a) p.dots[(size_t(r) * p.dots_cols + (n_a - p.col_begin)) * p.G + b] = da[v];
-                    if (ok_b) p.dots[(size_t(r) * p.dots_cols + (n_b - p.col_begin)) * p.G + b] = db[v];
-                }
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+
+    auto multiply = [&](int b, const Stage<TN, LDS_SCALES> &st) {
+        v4f s0 = st.s0, s1 = st.s1, s2 = st.s2, s3 = st.s3;
+        if (LDS_SCALES) {
+            const v4f *ls = reinterpret_cast<const v4f *>(tile_scales + b * 32 + 4 * h);
+            s0 = ls[0];
+            s1 = ls[2];
+            s2 = ls[4];
+            s3 = ls[6];
+        }
+        const float sc[16] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w, s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            v4i w = st.w[t];
+            if (FMT == 4) {
+                const int sh = h * 4;
+                w = v4i{nibbles_signed(w.x >> sh), nibbles_signed(w.y >> sh), nibbles_signed(w.z >> sh), nibbles_signed(w.w >> sh)};
             }
-            continue;
-        }
+            const v16i zero = {0};
+            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(st.a, w, zero, 0, 0, 0);
+            if (DOTS) {
+                const int n = n0 + 32 * t + i;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const float4 f = as4[v >> 2];
-            const float asv = (v & 3) == 0 ? f.x : (v & 3) == 1 ? f.y : (v & 3) == 2 ? f.z : f.w;
-            s0[v] = s0[v] + float(da[v]) * (ws_a * asv);
-            s1[v] = s1[v] + float(db[v]) * (ws_b * asv);
+                for (int v = 0; v < 16; v++) {
+                    const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (r < p.M && n < p.col_end) p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * p.G + b] = d[v];
+                }
+                continue;
+            }
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[t][v] = acc[t][v] + float(d[v]) * (st.ws[t] * sc[v]);
         }
+    };
+
+    // the ring: block b lives in stage b % kDepth; the fetch of block b + kDepth follows the
+    // multiply of block b (clamped at the last block, so the loop body has no branch around
+    // loads). Scheduling barriers keep each stage's work below the waits of younger loads.
+    Stage<TN, LDS_SCALES> st0, st1, st2, st3;
+    fetch(0, st0);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(min(1, B - 1), st1);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(min(2, B - 1), st2);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(min(3, B - 1), st3);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int b = 0; b < B; b += kDepth) {
+        multiply(b, st0);
+        fetch(min(b + 4, B - 1), st0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 1 < B) multiply(b + 1, st1);
+        fetch(min(b + 5, B - 1), st1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 2 < B) multiply(b + 2, st2);
+        fetch(min(b + 6, B - 1), st2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (b + 3 < B) multiply(b + 3, st3);
+        fetch(min(b + 7, B - 1), st3);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (DOTS) return;
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (r >= p.M) continue;
-        float *orow = p.out + size_t(r) * p.ld_out - p.col_begin;
-        if (ok_a) {
-            float y = s0[v];
-            if (p.bias && n_a < p.n_rows) y = y + p.bias[n_a];
-            orow[n_a] = p.accumulate ? orow[n_a] + y : y;
-        }
-        if (ok_b) {
-            float y = s1[v];
-            if (p.bias && n_b < p.n_rows) y = y + p.bias[n_b];
-            orow[n_b] = p.accumulate ? orow[n_b] + y : y;
+    for (int t = 0; t < TN; t++) {
+        const int n = n0 + 32 * t + i;
+        if (n >= p.col_end) continue;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (r >= p.M) continue;
+            float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+            float y = acc[t][v];
+            if (p.bias && n < p.n_rows) y = y + p.bias[n];
+            *o = p.accumulate ? *o + y : y;
         }
     }
 }
@@ -134,14 +190,25 @@ __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int
     as_t[id] = r < M ? as[size_t(r) * G + g] : 0.0f;
 }
 
-template <int FMT, int WM>
+// 32 x 64 tiles per wave where they still give every SIMD a wave or more, else 32 x 32.
+template <int FMT>
 int launch_tiles(const GemmParams &p, bool dots, hipStream_t s)
 {
-    constexpr int WN = 4 / WM;
     const int ncols = p.col_end - p.col_begin;
-    dim3 grid(unsigned((ncols + 64 * WN - 1) / (64 * WN)), unsigned((p.M + 32 * WM - 1) / (32 * WM)));
-    if (dots) gemm_kernel<FMT, WM, true><<<grid, 256, 0, s>>>(p);
-    else gemm_kernel<FMT, WM, false><<<grid, 256, 0, s>>>(p);
+    const long wide_waves = long((ncols + 63) / 64) * ((p.M + 31) / 32);
+    const size_t smem = size_t(p.B) * 32 * 4;
+    const bool lds = smem <= 64 * 1024;  // larger K keeps the scales in the ring
+    if (wide_waves >= 1024) {
+        dim3 grid(unsigned((ncols + 63) / 64), unsigned((p.M + 31) / 32));
+        if (dots) gemm_kernel<FMT, 2, true, false><<<grid, 64, 0, s>>>(p);
+        else if (lds) gemm_kernel<FMT, 2, false, true><<<grid, 64, smem, s>>>(p);
+        else gemm_kernel<FMT, 2, false, false><<<grid, 64, 0, s>>>(p);
+    } else {
+        dim3 grid(unsigned((ncols + 31) / 32), unsigned((p.M + 31) / 32));
+        if (dots) gemm_kernel<FMT, 1, true, false><<<grid, 64, 0, s>>>(p);
+        else if (lds) gemm_kernel<FMT, 1, false, true><<<grid, 64, smem, s>>>(p);
+        else gemm_kernel<FMT, 1, false, false><<<grid, 64, 0, s>>>(p);
+    }
     FG_HIP(hipGetLastError());
     return FG_OK;
 }
@@ -273,9 +340,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.dots = a.dots;
         p.dots_cols = p.col_end - p.col_begin;
         const bool dots = a.dots != nullptr;
-        const bool tall = M > 32;
-        if (t->dtype == FG_Q4B32) rc = tall ? launch_tiles<4, 2>(p, dots, s) : launch_tiles<4, 1>(p, dots, s);
-        else rc = tall ? launch_tiles<8, 2>(p, dots, s) : launch_tiles<8, 1>(p, dots, s);
+        rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, s) : launch_tiles<8>(p, dots, s);
     }
     hipError_t e = hipFreeAsync(ws, s);
     if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");

@@ -31,7 +31,8 @@ struct GemmParams {
     int col_begin, col_end;
     int n_rows;
     const int8_t *q;      // [M][K] levels
-    const float *as_t;    // [G][Mpad] activation scales, block-major
+    const float *as;      // [M][G] activation scales (row-major, 16-byte rows: staged in LDS)
+    const float *as_t;    // [G][Mpad] the same, block-major (when not staged)
     const float *bias;
     float *out;
     long ld_out;
@@ -76,11 +77,17 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     }
     const int B = p.B;
     if (LDS_SCALES) {
-        // rows m0 .. m0 + 31 of as_t for every block: 8 float4 per block
-        for (int e = lane; e < B * 8; e += 64) {
-            const int b = e >> 3, c = e & 7;
-            reinterpret_cast<v4f *>(tile_scales)[e] = *reinterpret_cast<const v4f *>(p.as_t + size_t(b) * p.Mpad + m0 + 4 * c);
+        // rows m0 .. m0 + 31 of as (rows past M re-read the last), transposed to [block][row]:
+        // lane l reads four blocks of row l % 32 and writes them to four consecutive-row slots
+        const float *srow = p.as + size_t(min(m0 + i, p.M - 1)) * p.G;
+        for (int c = h; c < B / 4; c += 2) {
+            const v4f v = *reinterpret_cast<const v4f *>(srow + 4 * c);
+            tile_scales[(4 * c) * 32 + i] = v.x;
+            tile_scales[(4 * c + 1) * 32 + i] = v.y;
+            tile_scales[(4 * c + 2) * 32 + i] = v.z;
+            tile_scales[(4 * c + 3) * 32 + i] = v.w;
         }
+        __syncthreads();
     }
 
     auto fetch = [&](int b, Stage<TN, LDS_SCALES> &st) {
@@ -192,12 +199,11 @@ __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int
 
 // 32 x 64 tiles per wave where they still give every SIMD a wave or more, else 32 x 32.
 template <int FMT>
-int launch_tiles(const GemmParams &p, bool dots, hipStream_t s)
+int launch_tiles(const GemmParams &p, bool dots, bool lds, hipStream_t s)
 {
     const int ncols = p.col_end - p.col_begin;
     const long wide_waves = long((ncols + 63) / 64) * ((p.M + 31) / 32);
     const size_t smem = size_t(p.B) * 32 * 4;
-    const bool lds = smem <= 64 * 1024;  // larger K keeps the scales in the ring
     if (wide_waves >= 1024) {
         dim3 grid(unsigned((ncols + 63) / 64), unsigned((p.M + 31) / 32));
         if (dots) gemm_kernel<FMT, 2, true, false><<<grid, 64, 0, s>>>(p);
@@ -295,12 +301,17 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
     if (t->dtype == FG_T2B128) return launch_t2(a, s);
     const int M = int(a.rows), K = int(t->cols), G = int(t->groups);
     const int Mpad = (M + 63) / 64 * 64;
-    // Workspace: levels (when the input is f32), scales, corrections, block-major scales.
+    const bool dots = a.dots != nullptr;
+    // The activation scales go to LDS per tile when a tile's fit in 64 KiB and their rows are
+    // whole float4s; otherwise the kernel reads a block-major copy.
+    const bool lds = !dots && size_t(G) * 32 * 4 <= 64 * 1024 && G % 4 == 0 &&
+                     (a.x || (reinterpret_cast<uintptr_t>(a.as) & 15) == 0);
+    // Workspace: levels, scales and corrections (when the input is f32), block-major scales.
     const size_t q_bytes = a.x ? (size_t(M) * K + 255) / 256 * 256 : 0;
     const size_t s_bytes = a.x ? (size_t(M) * G * 4 + 255) / 256 * 256 : 0;
-    const size_t t_bytes = size_t(G) * Mpad * 4;
+    const size_t t_bytes = (lds || dots) ? 0 : size_t(G) * Mpad * 4;
     void *ws = nullptr;
-    FG_HIP(hipMallocAsync(&ws, q_bytes + 2 * s_bytes + t_bytes, s));
+    if (q_bytes + s_bytes + t_bytes) FG_HIP(hipMallocAsync(&ws, q_bytes + 2 * s_bytes + t_bytes, s));
     int8_t *q = const_cast<int8_t *>(a.q);
     const float *as = a.as;
     char *base = static_cast<char *>(ws);
@@ -313,7 +324,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         as = sc;
     }
     float *as_t = reinterpret_cast<float *>(base + q_bytes + 2 * s_bytes);
-    if (rc == FG_OK) {
+    if (rc == FG_OK && t_bytes) {
         const size_t n = size_t(G) * Mpad;
         transpose_scales_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(as, M, G, Mpad, as_t);
         hipError_t e = hipGetLastError();
@@ -332,6 +343,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.col_end = int(a.quad_end * 4);
         p.n_rows = int(t->rows);
         p.q = q;
+        p.as = as;
         p.as_t = as_t;
         p.bias = a.bias;
         p.out = a.out;
@@ -339,11 +351,12 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.accumulate = a.accumulate;
         p.dots = a.dots;
         p.dots_cols = p.col_end - p.col_begin;
-        const bool dots = a.dots != nullptr;
-        rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, s) : launch_tiles<8>(p, dots, s);
+        rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, lds, s) : launch_tiles<8>(p, dots, lds, s);
     }
-    hipError_t e = hipFreeAsync(ws, s);
-    if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
+    if (ws) {
+        hipError_t e = hipFreeAsync(ws, s);
+        if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
+    }
     return rc;
 }
 

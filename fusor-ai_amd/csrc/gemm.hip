@@ -188,6 +188,96 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     }
 }
 
+// At most 16 rows: v_mfma_i32_16x16x32_i8, one wave per 16 x 16 tile, an eight-block ring.
+// Operand layout (16x16x32): lane l feeds row (or column) l % 16 with inputs 8·(l/16) .. +7 of
+// the block; result: lane l holds column l % 16, rows 4·(l/16) + v for v = 0..3.
+constexpr int kDepth16 = 8;
+
+template <int FMT, bool DOTS>
+__global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
+{
+    extern __shared__ __align__(16) float tile_scales[];  // [B][16]
+    constexpr int QB = FMT == 8 ? 128 : 64;
+    const int lane = threadIdx.x, i = lane & 15, s = lane >> 4;  // s: this lane's slice of 8 inputs
+    const int n0 = p.col_begin + int(blockIdx.x) * 16;
+    const int row = min(i, p.M - 1);
+    const int n = n0 + i, nc = min(n, p.col_end - 1);
+    const int B = p.B;
+    const int8_t *arow = p.q + size_t(row) * p.K + 8 * s;
+    // Q8 row-block: 32 levels; Q4: byte j holds inputs j and j + 16 in its nibbles
+    const int8_t *wrow = p.codes + size_t(nc >> 2) * B * QB + (nc & 3) * (QB / 4) + (FMT == 8 ? 8 * s : 8 * (s & 1));
+    const int shift = FMT == 8 ? 0 : 4 * (s >> 1);
+    const float *wsrow = p.wscales + size_t(nc >> 2) * p.G * 4 + (nc & 3);
+    if (!DOTS) {
+        // the rows' scales, transposed to [block][row] (rows past M re-read the last)
+        const float *srow = p.as + size_t(row) * p.G;
+        for (int c = s; c < B / 4; c += 4) {
+            const v4f v = *reinterpret_cast<const v4f *>(srow + 4 * c);
+            tile_scales[(4 * c) * 16 + i] = v.x;
+            tile_scales[(4 * c + 1) * 16 + i] = v.y;
+            tile_scales[(4 * c + 2) * 16 + i] = v.z;
+            tile_scales[(4 * c + 3) * 16 + i] = v.w;
+        }
+        __syncthreads();
+    }
+    struct St {
+        long a, w;
+        float ws;
+    };
+    auto fetch = [&](int b, St &st) {
+        st.a = *reinterpret_cast<const long *>(arow + b * 32);
+        st.w = *reinterpret_cast<const long *>(wrow + size_t(b) * QB);
+        st.ws = wsrow[size_t(b) * 4];
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto multiply = [&](int b, const St &st) {
+        long w = st.w;
+        if (FMT == 4) {
+            const int lo = nibbles_signed(int(w) >> shift), hi = nibbles_signed(int(w >> 32) >> shift);
+            w = long(unsigned(lo)) | (long(hi) << 32);
+        }
+        const v4i zero = {0, 0, 0, 0};
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.a, w, zero, 0, 0, 0);
+        if (DOTS) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = 4 * s + v;
+                if (r < p.M && n < p.col_end) p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * p.G + b] = d[v];
+            }
+            return;
+        }
+        const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + b * 16 + 4 * s);
+        acc[0] = acc[0] + float(d[0]) * (st.ws * sc.x);
+        acc[1] = acc[1] + float(d[1]) * (st.ws * sc.y);
+        acc[2] = acc[2] + float(d[2]) * (st.ws * sc.z);
+        acc[3] = acc[3] + float(d[3]) * (st.ws * sc.w);
+    };
+    St ring[kDepth16];
+#pragma unroll
+    for (int k = 0; k < kDepth16; k++) {
+        fetch(min(k, B - 1), ring[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int b = 0; b < B; b += kDepth16) {
+#pragma unroll
+        for (int k = 0; k < kDepth16; k++) {
+            if (b + k < B) multiply(b + k, ring[k]);
+            fetch(min(b + k + kDepth16, B - 1), ring[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (DOTS || n >= p.col_end) return;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int r = 4 * s + v;
+        if (r >= p.M) continue;
+        float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+        float y = acc[v];
+        if (p.bias && n < p.n_rows) y = y + p.bias[n];
+        *o = p.accumulate ? *o + y : y;
+    }
+}
+
 // as [M][G] -> as_t [G][Mpad] (zeros past M).
 __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int G, int Mpad, float *__restrict__ as_t)
 {
@@ -202,6 +292,13 @@ template <int FMT>
 int launch_tiles(const GemmParams &p, bool dots, bool lds, hipStream_t s)
 {
     const int ncols = p.col_end - p.col_begin;
+    if (p.M <= 16 && (dots || lds)) {
+        const dim3 grid(unsigned((ncols + 15) / 16));
+        if (dots) gemm16_kernel<FMT, true><<<grid, 64, 0, s>>>(p);
+        else gemm16_kernel<FMT, false><<<grid, 64, size_t(p.B) * 16 * 4, s>>>(p);
+        FG_HIP(hipGetLastError());
+        return FG_OK;
+    }
     const long wide_waves = long((ncols + 63) / 64) * ((p.M + 31) / 32);
     const size_t smem = size_t(p.B) * 32 * 4;
     if (wide_waves >= 1024) {

@@ -16,52 +16,30 @@ __device__ __forceinline__ void code_position(int cpb, int lane, int input, int 
     shift = bits * (chunk / words);
 }
 
-// Reference quad blocks to device quad blocks (and back with `inverse`): one thread per
-// (quad, block).
-__global__ void relayout_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int dtype,
-                                size_t quad_blocks, int inverse)
+// Reference quad blocks to device quad blocks (and back with `inverse`). In every format the
+// code of lane L, input k sits in the reference at byte (c % W)·16 + 4L + k % 4 (c = k / 4, W = 8 /
+// codes per byte), and the device's packing puts the codes sharing a reference byte into the same
+// device byte: device dword j of lane L is reference dword (j·16 + 4L) / 4 of the quad block, a
+// transpose of dwords (quant.rs:89-97). Q7b32 also moves the codes to signed levels, u - 64, byte
+// by byte (wrapping, so that any byte round-trips). One thread per device dword, coalesced.
+__global__ void relayout_kernel(const uint32_t *__restrict__ src, uint32_t *__restrict__ dst, int dtype, size_t dwords,
+                                int inverse)
 {
-    size_t qb = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (qb >= quad_blocks) return;
-    int cpb = dtype == FG_Q4B32 ? 2 : dtype == FG_T2B128 ? 4 : 1;
-    int qbytes = 128 / cpb;
-    int mask = 0xff >> (8 - 8 / cpb);
-    uint8_t ref[128];
-    uint8_t dev[128];
-    const uint8_t *in = src + qb * qbytes;
+    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= dwords) return;
+    const int per_lane = dtype == FG_Q4B32 ? 4 : dtype == FG_T2B128 ? 2 : 8;  // device dwords per lane row
+    const size_t quad_block = id / (4 * per_lane);
+    const int r = int(id % (4 * per_lane)), lane = r / per_lane, j = r % per_lane;
+    const size_t dev = id, ref = quad_block * (4 * per_lane) + size_t(j) * 4 + lane;
+    constexpr uint32_t H = 0x80808080u;
     if (!inverse) {
-        for (int i = 0; i < qbytes; i++) ref[i] = in[i];
-        for (int i = 0; i < qbytes; i++) dev[i] = 0;
-        for (int lane = 0; lane < 4; lane++) {
-            for (int k = 0; k < 32; k++) {
-                int byte, shift;
-                code_position(cpb, lane, k, byte, shift);
-                int u = (ref[byte] >> shift) & mask;
-                if (dtype == FG_Q7B32) dev[lane * 32 + k] = uint8_t(int8_t(u - 64));
-                else if (dtype == FG_Q8B32) dev[lane * 32 + k] = uint8_t(u);
-                else if (dtype == FG_Q4B32) dev[lane * 16 + (k & 15)] |= uint8_t(u << (4 * (k >> 4)));
-                else dev[lane * 8 + (k & 7)] |= uint8_t(u << (2 * (k >> 3)));
-            }
-        }
-        uint8_t *out = dst + qb * qbytes;
-        for (int i = 0; i < qbytes; i++) out[i] = dev[i];
+        uint32_t x = src[ref];
+        if (dtype == FG_Q7B32) x = ((x | H) - 0x40404040u) ^ ((x ^ 0xBFBFBFBFu) & H);  // bytes u - 64
+        dst[dev] = x;
     } else {
-        for (int i = 0; i < qbytes; i++) dev[i] = in[i];
-        for (int i = 0; i < qbytes; i++) ref[i] = 0;
-        for (int lane = 0; lane < 4; lane++) {
-            for (int k = 0; k < 32; k++) {
-                int u;
-                if (dtype == FG_Q7B32) u = int(int8_t(dev[lane * 32 + k])) + 64;
-                else if (dtype == FG_Q8B32) u = dev[lane * 32 + k];
-                else if (dtype == FG_Q4B32) u = (dev[lane * 16 + (k & 15)] >> (4 * (k >> 4))) & 15;
-                else u = (dev[lane * 8 + (k & 7)] >> (2 * (k >> 3))) & 3;
-                int byte, shift;
-                code_position(cpb, lane, k, byte, shift);
-                ref[byte] |= uint8_t(u << shift);
-            }
-        }
-        uint8_t *out = dst + qb * qbytes;
-        for (int i = 0; i < qbytes; i++) out[i] = ref[i];
+        uint32_t x = src[dev];
+        if (dtype == FG_Q7B32) x = ((x & 0x7F7F7F7Fu) + 0x40404040u) ^ (x & H);  // bytes level + 64
+        dst[ref] = x;
     }
 }
 
@@ -273,20 +251,20 @@ int launch_qmatrix_set(fg_table *t, size_t first, size_t count, size_t b0, size_
 
 int launch_relayout(const uint8_t *ref_codes, fg_table *t, hipStream_t s)
 {
-    size_t n = t->quads * t->blocks;
+    const size_t n = t->code_bytes / 4;
     if (n == 0) return FG_OK;
-    unsigned grid = unsigned((n + 255) / 256);
-    relayout_kernel<<<grid, 256, 0, s>>>(ref_codes, reinterpret_cast<uint8_t *>(t->codes), t->dtype, n, 0);
+    relayout_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(ref_codes),
+                                                              reinterpret_cast<uint32_t *>(t->codes), t->dtype, n, 0);
     FG_HIP(hipGetLastError());
     return FG_OK;
 }
 
 int launch_unrelayout(const fg_table *t, uint8_t *ref_codes, hipStream_t s)
 {
-    size_t n = t->quads * t->blocks;
+    const size_t n = t->code_bytes / 4;
     if (n == 0) return FG_OK;
-    unsigned grid = unsigned((n + 255) / 256);
-    relayout_kernel<<<grid, 256, 0, s>>>(reinterpret_cast<const uint8_t *>(t->codes), ref_codes, t->dtype, n, 1);
+    relayout_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(t->codes),
+                                                              reinterpret_cast<uint32_t *>(ref_codes), t->dtype, n, 1);
     FG_HIP(hipGetLastError());
     return FG_OK;
 }

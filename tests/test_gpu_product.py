@@ -271,6 +271,31 @@ def test_int4_shape_bit_exact(fk, rows):
     assert same_bits(got[sample], want), first_mismatch(got[sample], want)
 
 
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+@pytest.mark.parametrize("rows", [5, 11, 16])
+def test_small_batch_over_whole_tiles_bit_exact(fk, dtype, rows):
+    """5-16 rows with whole tiles of 16 groups (the LDS-staged small-batch kernel): every row and
+    column, a column range with bias, and the residual form."""
+    import torch
+    n, k = 100, 512
+    data = synthetic_table(dtype, n, k, seed=rows + 3 * dtype)
+    t = table(fk, dtype, n, k, data)
+    x = activations(rows, k, seed=rows, outliers=0.02)
+    assert same_bits(gpu_product(fk, t, x, rows), oracle_product(dtype, n, k, data, x, rows))
+    bias = np.random.default_rng(2).standard_normal(n).astype(np.float32)
+    got = gpu_product(fk, t, x, rows, cols=range(16, 100), bias=bias)
+    assert same_bits(got, oracle_product(dtype, n, k, data, x, rows, 16, 100, bias=bias))
+    h0 = np.random.default_rng(3).standard_normal((rows, n)).astype(np.float32)
+    h = dev(h0)
+    lin = fk.Linear(t, None)
+    inp = fk.QuantizedRows().input(t.matrix(), dev(x.reshape(-1)))
+    fk.project_residual_input(fk.Ctx(0, 1), lin, inp, h)
+    full = oracle_product(dtype, n, k, data, x, rows)[:, :n]
+    want_h = h0.copy()
+    want_h[:, :96] = (h0[:, :96] + full[:, :96]).astype(np.float32)
+    assert same_bits(host(h), want_h)
+
+
 def test_batched_rows_equal_row_by_row_products(fk):
     """A size-independent property: the matrix-core path and the matrix-vector path are the same
     function of each row."""

@@ -188,10 +188,13 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     }
 }
 
-// At most 16 rows: v_mfma_i32_16x16x32_i8, one wave per 16 x 16 tile, an eight-block ring.
-// Operand layout (16x16x32): lane l feeds row (or column) l % 16 with inputs 8·(l/16) .. +7 of
-// the block; result: lane l holds column l % 16, rows 4·(l/16) + v for v = 0..3.
-constexpr int kDepth16 = 8;
+// At most 16 rows: v_mfma_i32_16x16x32_i8, one wave per 16 x 16 tile. Weights, their scales and
+// the activations run kDepthW blocks ahead in rings of registers (loads complete in order, so
+// the activations' ring is as deep as the weights'). Deeper rings measured slower: the 16
+// activation rows of every block cost a cache line each per wave, and that request rate, not
+// the bytes in flight, bounds this shape. Operand layout (16x16x32): lane l feeds row (or column) l % 16 with inputs
+// 8·(l/16) .. +7 of the block; result: lane l holds column l % 16, rows 4·(l/16) + v, v = 0..3.
+constexpr int kDepthW = 8, kDepthA = 8;
 
 template <int FMT, bool DOTS>
 __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
@@ -220,49 +223,49 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
         }
         __syncthreads();
     }
-    struct St {
-        long a, w;
-        float ws;
-    };
-    auto fetch = [&](int b, St &st) {
-        st.a = *reinterpret_cast<const long *>(arow + b * 32);
-        st.w = *reinterpret_cast<const long *>(wrow + size_t(b) * QB);
-        st.ws = wsrow[size_t(b) * 4];
-    };
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto multiply = [&](int b, const St &st) {
-        long w = st.w;
-        if (FMT == 4) {
-            const int lo = nibbles_signed(int(w) >> shift), hi = nibbles_signed(int(w >> 32) >> shift);
-            w = long(unsigned(lo)) | (long(hi) << 32);
-        }
-        const v4i zero = {0, 0, 0, 0};
-        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.a, w, zero, 0, 0, 0);
-        if (DOTS) {
+    long rw[kDepthW], ra[kDepthA];
+    float rs[kDepthW];
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int r = 4 * s + v;
-                if (r < p.M && n < p.col_end) p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * p.G + b] = d[v];
-            }
-            return;
-        }
-        const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + b * 16 + 4 * s);
-        acc[0] = acc[0] + float(d[0]) * (st.ws * sc.x);
-        acc[1] = acc[1] + float(d[1]) * (st.ws * sc.y);
-        acc[2] = acc[2] + float(d[2]) * (st.ws * sc.z);
-        acc[3] = acc[3] + float(d[3]) * (st.ws * sc.w);
-    };
-    St ring[kDepth16];
-#pragma unroll
-    for (int k = 0; k < kDepth16; k++) {
-        fetch(min(k, B - 1), ring[k]);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < kDepthW; k++) {
+        const int bb = min(k, B - 1);
+        rw[k] = *reinterpret_cast<const long *>(wrow + size_t(bb) * QB);
+        rs[k] = wsrow[size_t(bb) * 4];
     }
-    for (int b = 0; b < B; b += kDepth16) {
 #pragma unroll
-        for (int k = 0; k < kDepth16; k++) {
-            if (b + k < B) multiply(b + k, ring[k]);
-            fetch(min(b + k + kDepth16, B - 1), ring[k]);
+    for (int k = 0; k < kDepthA; k++) ra[k] = *reinterpret_cast<const long *>(arow + min(k, B - 1) * 32);
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < B; b += kDepthW) {
+#pragma unroll
+        for (int k = 0; k < kDepthW; k++) {
+            const int bb = b + k;
+            if (bb < B) {
+                long w = rw[k];
+                if (FMT == 4) {
+                    const int lo = nibbles_signed(int(w) >> shift), hi = nibbles_signed(int(w >> 32) >> shift);
+                    w = long(unsigned(lo)) | (long(hi) << 32);
+                }
+                const v4i zero = {0, 0, 0, 0};
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ra[k % kDepthA], w, zero, 0, 0, 0);
+                if (DOTS) {
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int r = 4 * s + v;
+                        if (r < p.M && n < p.col_end) p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * p.G + bb] = d[v];
+                    }
+                } else {
+                    const float ws = rs[k];
+                    const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + bb * 16 + 4 * s);
+                    acc[0] = acc[0] + float(d[0]) * (ws * sc.x);
+                    acc[1] = acc[1] + float(d[1]) * (ws * sc.y);
+                    acc[2] = acc[2] + float(d[2]) * (ws * sc.z);
+                    acc[3] = acc[3] + float(d[3]) * (ws * sc.w);
+                }
+            }
+            const int nw = min(bb + kDepthW, B - 1), na = min(bb + kDepthA, B - 1);
+            rw[k] = *reinterpret_cast<const long *>(wrow + size_t(nw) * QB);
+            rs[k] = wsrow[size_t(nw) * 4];
+            ra[k % kDepthA] = *reinterpret_cast<const long *>(arow + na * 32);
             __builtin_amdgcn_sched_barrier(0);
         }
     }

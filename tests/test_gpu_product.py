@@ -296,6 +296,19 @@ def test_small_batch_over_whole_tiles_bit_exact(fk, dtype, rows):
     assert same_bits(host(h), want_h)
 
 
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+def test_batched_product_with_subnormal_scale_products(fk, dtype):
+    """Weight scales near 1e-8 and activations near 1e-30: every fl(ws·as) is subnormal (about
+    1e-41) while the terms fl(D·p) are normal; the batched path keeps the reference's bits."""
+    n, k, rows = 70, 256, 40
+    data = synthetic_table(dtype, n, k, seed=dtype, scale_lo=1e-9, scale_hi=1e-8)
+    t = table(fk, dtype, n, k, data)
+    x = (activations(rows, k, seed=3) * np.float32(1e-30)).astype(np.float32)
+    want = oracle_product(dtype, n, k, data, x, rows)
+    assert same_bits(gpu_product(fk, t, x, rows), want), first_mismatch(gpu_product(fk, t, x, rows), want)
+    assert np.all(np.isfinite(want)) and np.any(want != 0)
+
+
 def test_batched_rows_equal_row_by_row_products(fk):
     """A size-independent property: the matrix-core path and the matrix-vector path are the same
     function of each row."""

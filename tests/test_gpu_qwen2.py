@@ -125,6 +125,23 @@ def test_small_decoder_fast_mode_within_tolerance(fk, dtype):
     assert rel_l2(got[1], want[1]) < FAST_TOLERANCE
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(64, 4, 1), (128, 2, 2), (32, 6, 3)])
+def test_decoder_head_sizes_and_many_key_chunks(fk, head_dim, heads, kv_heads):
+    """Every head size the decoder takes, and positions past several 64-key chunks of the
+    parallel-order attention: exact mode bit-identical, parallel order within tolerance."""
+    shape = dict(hidden=256, layers=2, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=512, vocab=64,
+                 capacity=300)
+    params = build(O.Q7B32, seed=head_dim, synthetic=False, **shape)
+    for position in (63, 64, 200, 299):
+        got, want = run_both(fk, O.Q7B32, params, token=9, position=position, exact=True)
+        assert same_bits(got[0], want[0]), ("hidden", position)
+        assert same_bits(got[1], want[1]), ("logits", position)
+        assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+        got, want = run_both(fk, O.Q7B32, params, token=9, position=position, exact=False)
+        assert rel_l2(got[0], want[0]) < FAST_TOLERANCE, ("fast hidden", position)
+        assert rel_l2(got[1], want[1]) < FAST_TOLERANCE, ("fast logits", position)
+
+
 def test_layer_forward_equals_the_oracle_layer(fk):
     import torch
     dtype = O.Q7B32

@@ -132,6 +132,151 @@ __device__ __forceinline__ int quantize_level(float x, float d)
 // `extreme == 0 ? 1 : extreme / level` (quant.rs:126-128).
 __device__ __forceinline__ float group_scale(float extreme, float level) { return extreme == 0.0f ? 1.0f : extreme / level; }
 
+// The levels of groups of 32 values (activation quantization, scalar.rs:48-66, arch/mod.rs:223-228)
+// held by 8 aligned lanes, four values each, to the bit of the reference's IEEE arithmetic.
+//
+// A correctly rounded a / b costs about a dozen instructions: the compiler's expansion scales both
+// operands (v_div_scale), refines a reciprocal of the scaled divisor, corrects the quotient with
+// fused multiply-adds and undoes the scaling (v_div_fmas, v_div_fixup). The scaling is the identity
+// unless an operand or the quotient is near the ends of the exponent range, so where it provably is,
+// the same reciprocal and correction steps alone give the same quotient, and a divisor's
+// reciprocal is shared by the values it divides:
+//   d = amax / 127 for amax in [2^-52, 2^66];
+//   x / d for d in [2^-60, 2^60] and |x| <= amax (|x / d| < 128): the scaling acts only when
+//   |x / d| < 2^-43 or |x| < 2^-103, and those quotients are below 1/4, so their level is 0 either
+//   way (the remainders of every larger quotient stay normal).
+// Groups outside that range take the IEEE division itself.
+__device__ __forceinline__ int level_of(float t)
+{
+    float r = __builtin_rintf(t);
+    if (r != r) return 0;
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    return int(r);
+}
+
+// The reciprocal of b refined as the division expansion refines it (v_rcp_f32 then one step).
+__device__ __forceinline__ float refined_reciprocal(float b)
+{
+    const float r0 = __builtin_amdgcn_rcpf(b);
+    return __builtin_fmaf(__builtin_fmaf(-b, r0, 1.0f), r0, r0);
+}
+// a / b from the refined reciprocal r of b: the expansion's two correction steps.
+__device__ __forceinline__ float corrected_quotient(float a, float b, float r)
+{
+    const float q = a * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-b, q, a), r, q);
+    return __builtin_fmaf(__builtin_fmaf(-b, q1, a), r, q1);
+}
+// The level of a quotient with |t| < 128 or NaN: v_cvt_i32_f32 converts NaN to 0, the reference's
+// saturating cast; rounding ties to even first.
+__device__ __forceinline__ int level_in_range(float t)
+{
+    int i;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(__builtin_rintf(t)));
+    return i;
+}
+
+// The scale amax / 127 of a group and the levels of four of its values, branching per lane.
+__device__ __forceinline__ float scale_and_levels(float amax, float x0, float x1, float x2, float x3, int &l0, int &l1,
+                                                  int &l2, int &l3)
+{
+    if (amax >= 0x1p-52f && amax <= 0x1p66f) {
+        float c = 127.0f;
+        asm("" : "+v"(c));  // the divisor's reciprocal from v_rcp_f32 at run time, as the expansion takes it
+        const float d = corrected_quotient(amax, c, refined_reciprocal(c));
+        const float r = refined_reciprocal(d);
+        l0 = level_in_range(corrected_quotient(x0, d, r));
+        l1 = level_in_range(corrected_quotient(x1, d, r));
+        l2 = level_in_range(corrected_quotient(x2, d, r));
+        l3 = level_in_range(corrected_quotient(x3, d, r));
+        return d;
+    }
+    const float d = group_scale(amax, 127.0f);
+    l0 = quantize_level(x0, d);
+    l1 = quantize_level(x1, d);
+    l2 = quantize_level(x2, d);
+    l3 = quantize_level(x3, d);
+    return d;
+}
+
+struct Group8 {
+    int packed;  // this lane's four levels, lowest first
+    int total;   // the sum of the group's 32 levels (every lane of the group)
+    float d;     // the group's scale
+};
+
+// Maximum over aligned groups of 8 lanes of floats that are >= 0 and not NaN: their bits order as
+// unsigned integers do, so one fused DPP integer maximum per step.
+__device__ __forceinline__ float max8_nonneg(float v)
+{
+    unsigned u = __float_as_uint(v);
+    u = max(u, unsigned(xor1(int(u))));
+    u = max(u, unsigned(xor2(int(u))));
+    return __uint_as_float(max(u, unsigned(mirror8(int(u)))));
+}
+
+// N groups at once (independent instruction streams the scheduler interleaves). Every lane of the
+// wave runs it (the group reductions read neighbouring lanes); callers predicate the stores.
+template <int N>
+__device__ __forceinline__ void quantize_groups(const v4f *v, Group8 *out)
+{
+    float amax[N];
+    bool fast = true;
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        // fold(0, max |x|) with NaN ignored (f32::max): fmaxf keeps the non-NaN operand
+        float a = fmaxf(fmaxf(fabsf(v[n].x), fabsf(v[n].y)), fmaxf(fabsf(v[n].z), fabsf(v[n].w)));
+        amax[n] = max8_nonneg(fmaxf(a, 0.0f));
+        fast = fast && amax[n] >= 0x1p-52f && amax[n] <= 0x1p66f;
+    }
+    // the shared-reciprocal path for every group, then (rarely) the IEEE division for groups outside
+    // its range, so the range test is off the arithmetic's critical path
+    int l[N][4];
+    float c = 127.0f;
+    asm("" : "+v"(c));  // the divisor's reciprocal from v_rcp_f32 at run time, as the expansion takes it
+    const float r127 = refined_reciprocal(c);
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        const float d = corrected_quotient(amax[n], c, r127);
+        const float r = refined_reciprocal(d);
+        out[n].d = d;
+        l[n][0] = level_in_range(corrected_quotient(v[n].x, d, r));
+        l[n][1] = level_in_range(corrected_quotient(v[n].y, d, r));
+        l[n][2] = level_in_range(corrected_quotient(v[n].z, d, r));
+        l[n][3] = level_in_range(corrected_quotient(v[n].w, d, r));
+    }
+    if (!__all(fast)) {
+#pragma unroll
+        for (int n = 0; n < N; n++) {
+            if (!(amax[n] >= 0x1p-52f && amax[n] <= 0x1p66f)) {
+                const float d = amax[n] == 0.0f ? 1.0f : amax[n] / 127.0f;
+                out[n].d = d;
+                l[n][0] = level_of(v[n].x / d);
+                l[n][1] = level_of(v[n].y / d);
+                l[n][2] = level_of(v[n].z / d);
+                l[n][3] = level_of(v[n].w / d);
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        out[n].packed = (l[n][0] & 0xff) | ((l[n][1] & 0xff) << 8) | ((l[n][2] & 0xff) << 16) | ((l[n][3] & 0xff) << 24);
+        out[n].total = sum8(l[n][0] + l[n][1] + l[n][2] + l[n][3]);
+    }
+}
+
+// A group's levels, scale and correction (−zp · Σ levels) to staging arrays indexed by group.
+__device__ __forceinline__ void store_group8(const Group8 &g, int zp, int grp, int8_t *q, float *scales, int32_t *corr)
+{
+    const int sub = threadIdx.x & 7;
+    reinterpret_cast<int *>(q)[grp * 8 + sub] = g.packed;
+    if (sub == 0) {
+        scales[grp] = g.d;
+        corr[grp] = -zp * g.total;
+    }
+}
+
+
 // Pack four int8 levels into one dword, lowest first.
 __device__ __forceinline__ int pack4(int a, int b, int c, int d)
 {

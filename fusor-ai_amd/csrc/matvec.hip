@@ -156,19 +156,26 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
     }
 }
 
-// Quantize one group of 32 held by 8 lanes (four values each) at `grp` of the staged rows.
-__device__ __forceinline__ void quantize8(v4f v, int zp, int grp, int8_t *q, float *scales, int32_t *corr)
+// Quantize `n` float4 slots per thread (slot k of thread t is float4 t + k·256 of the staged rows;
+// eight consecutive threads hold one group of 32) into the staging arrays. Slots are taken two at
+// a time, so that two groups' arithmetic interleaves; a wave skips the slots none of its lanes
+// holds, and each lane stores only the groups it holds.
+template <int S>
+__device__ __forceinline__ void quantize_slots(const v4f (&v)[S], int n4, int zp, int8_t *q, float *scales, int32_t *corr)
 {
-    const int sub = threadIdx.x & 7;
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = max8(fmaxf(0.0f, amax));
-    const float d = group_scale(amax, 127.0f);
-    const int l0 = quantize_level(v.x, d), l1 = quantize_level(v.y, d), l2 = quantize_level(v.z, d), l3 = quantize_level(v.w, d);
-    const int sum = sum8(l0 + l1 + l2 + l3);
-    reinterpret_cast<int *>(q)[grp * 8 + sub] = pack4(l0, l1, l2, l3);
-    if (sub == 0) {
-        scales[grp] = d;
-        corr[grp] = -zp * sum;
+    const int tid = threadIdx.x, first = tid & ~63;
+#pragma unroll
+    for (int k = 0; k < S; k += 2) {
+        if (k + 1 < S && first + (k + 1) * kThreads < n4) {
+            Group8 gr[2];
+            quantize_groups<2>(&v[k], gr);
+            if (tid + k * kThreads < n4) store_group8(gr[0], zp, (tid + k * kThreads) / 8, q, scales, corr);
+            if (tid + (k + 1) * kThreads < n4) store_group8(gr[1], zp, (tid + (k + 1) * kThreads) / 8, q, scales, corr);
+        } else if (first + k * kThreads < n4) {
+            Group8 gr[1];
+            quantize_groups<1>(&v[k], gr);
+            if (tid + k * kThreads < n4) store_group8(gr[0], zp, (tid + k * kThreads) / 8, q, scales, corr);
+        }
     }
 }
 
@@ -202,22 +209,17 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             act_c[i] = p.corr[i];
         }
     } else if (IN == IN_F32) {
-        // 8 lanes per group of 32 (quantize_rows): thread t holds float4 t of the rows; every lane
-        // of an 8-lane group is active together (the float4 count is a multiple of 8)
+        // 8 lanes per group of 32 (quantize_rows): thread t holds float4s t, t + 256, ... of the rows
         const int n4 = R * K / 4;
-#define FG_Q8(v, k) \
-    if (tid + (k) * kThreads < n4) quantize8((v), p.zp, (tid + (k) * kThreads) / 8, act_q, act_s, act_c);
-        FG_Q8(g.f0, 0)
-        FG_Q8(g.f1, 1)
-        FG_Q8(g.f2, 2)
-        FG_Q8(g.f3, 3)
-        FG_Q8(g.f4, 4)
-        FG_Q8(g.f5, 5)
-        FG_Q8(g.f6, 6)
-        FG_Q8(g.f7, 7)
-#undef FG_Q8
-        for (int i = tid + 8 * kThreads; i < n4; i += kThreads)
-            quantize8(reinterpret_cast<const v4f *>(p.x)[i], p.zp, i / 8, act_q, act_s, act_c);
+        const v4f slots[8] = {g.f0, g.f1, g.f2, g.f3, g.f4, g.f5, g.f6, g.f7};
+        quantize_slots<8>(slots, n4, p.zp, act_q, act_s, act_c);
+        for (int i0 = 8 * kThreads; i0 < n4; i0 += kThreads) {  // rows past 8 float4s per thread
+            const int i = min(tid + i0, n4 - 1);
+            const v4f rest[1] = {reinterpret_cast<const v4f *>(p.x)[i]};
+            Group8 gr[1];
+            quantize_groups<1>(rest, gr);
+            if (tid + i0 < n4) store_group8(gr[0], p.zp, i / 8, act_q, act_s, act_c);
+        }
     } else if (IN == IN_ATTN) {
         // the chunks' softmax states merged (flash decoding): M = max m_c, L = Σ l_c·e^(m_c − M),
         // out = Σ acc_c·e^(m_c − M) / L; then the row quantized (8 lanes per group of 32)
@@ -235,7 +237,8 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
                 o = o + g.pa[c] * e;
             }
         }
-        if (tid < K / 4) quantize8(o / L, p.zp, tid / 8, act_q, act_s, act_c);
+        const v4f merged[1] = {o / L};
+        quantize_slots<1>(merged, K / 4, p.zp, act_q, act_s, act_c);
     } else {
         // rms_norm (ops.rs:7-16): mean of squares, 1/sqrt(mean + eps), x·inverse·weight; then the
         // quantization of the normed row. Thread t holds float4s t, t + 256, ... of the row, so
@@ -282,10 +285,8 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             total = ((red[0] + red[1]) + red[2]) + red[3];
         }
         const float inverse = 1.0f / sqrtf(total / float(K) + p.eps);
-        if (tid < n4) quantize8(g.f0 * inverse * g.w0, p.zp, tid / 8, act_q, act_s, act_c);
-        if (tid + kThreads < n4) quantize8(g.f1 * inverse * g.w1, p.zp, (tid + kThreads) / 8, act_q, act_s, act_c);
-        if (tid + 2 * kThreads < n4) quantize8(g.f2 * inverse * g.w2, p.zp, (tid + 2 * kThreads) / 8, act_q, act_s, act_c);
-        if (tid + 3 * kThreads < n4) quantize8(g.f3 * inverse * g.w3, p.zp, (tid + 3 * kThreads) / 8, act_q, act_s, act_c);
+        const v4f normed[4] = {g.f0 * inverse * g.w0, g.f1 * inverse * g.w1, g.f2 * inverse * g.w2, g.f3 * inverse * g.w3};
+        quantize_slots<4>(normed, n4, p.zp, act_q, act_s, act_c);
     }
 }
 
@@ -363,36 +364,61 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         }
     };
 
+    // A batch is consumed U chunks at a time: the chunks' activation reads from LDS first, then
+    // their dots and term stores. LDS reads are not moved above possibly aliasing LDS stores, so
+    // reading per chunk would serialize two LDS round trips per chunk.
+    constexpr int U = R == 1 ? (FMT == 8 ? kBatch : (kBatch + 1) / 2) : (R == 2 ? (kBatch < 4 ? kBatch : 4) : (kBatch < 2 ? kBatch : 2));
     auto consume = [&](int b, const int4 *w, const float *ws) {
 #pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-            const int ql = ccur.ql, blk = ccur.blk;
-            advance(ccur);
-            if (b * kBatch + u >= mine) continue;  // uniform across the wave
-            const bool valid = ql < nq;
+        for (int u0 = 0; u0 < kBatch; u0 += U) {
+            int qls[U], blks[U];
+            int4 a0[U][R], a1[U][R];
+            float asc[U][R];
+            int acr[U][R];
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                int D;
-                if (FMT == 8) {
-                    const int4 a = *reinterpret_cast<const int4 *>(act_q + r * K + blk * 32 + h * 16);
-                    D = dot16(w[u], a);
-                    D += xor1(D);  // the row-block's other half
-                } else {
-                    const int bb = blk;
-                    const int4 a0 = *reinterpret_cast<const int4 *>(act_q + r * K + bb * 32);
-                    const int4 a1 = *reinterpret_cast<const int4 *>(act_q + r * K + bb * 32 + 16);
-                    const int4 lo = make_int4(w[u].x & 0x0F0F0F0F, w[u].y & 0x0F0F0F0F, w[u].z & 0x0F0F0F0F, w[u].w & 0x0F0F0F0F);
-                    const int4 hi = make_int4((w[u].x >> 4) & 0x0F0F0F0F, (w[u].y >> 4) & 0x0F0F0F0F,
-                                              (w[u].z >> 4) & 0x0F0F0F0F, (w[u].w >> 4) & 0x0F0F0F0F);
-                    D = dot16(lo, a0) + dot16(hi, a1) + act_c[r * G + bb];
-                }
-                if (valid && h == 0) {
-                    if (OUT == OUT_DOTS) {
-                        const int n = (base + ql * qs) * 4 + L;
-                        p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * G + blk] = D;
+            for (int v = 0; v < U; v++) {
+                qls[v] = ccur.ql;
+                blks[v] = ccur.blk;
+                advance(ccur);
+                const int blk = blks[v];  // < B always: every read is in bounds
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    if (FMT == 8) {
+                        a0[v][r] = *reinterpret_cast<const int4 *>(act_q + r * K + blk * 32 + h * 16);
                     } else {
-                        const float scale = ws[u] * act_s[r * G + blk];
-                        terms[((tb * R + r) * NW + ql * 4 + L) * Gp + blk] = float(D) * scale;
+                        a0[v][r] = *reinterpret_cast<const int4 *>(act_q + r * K + blk * 32);
+                        a1[v][r] = *reinterpret_cast<const int4 *>(act_q + r * K + blk * 32 + 16);
+                        acr[v][r] = act_c[r * G + blk];
+                    }
+                    if (OUT != OUT_DOTS) asc[v][r] = act_s[r * G + blk];
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < U; v++) {
+                const int u = u0 + v;
+                if (b * kBatch + u >= mine) continue;  // uniform across the wave
+                const int ql = qls[v], blk = blks[v];
+                const bool valid = ql < nq;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    int D;
+                    if (FMT == 8) {
+                        D = dot16(w[u], a0[v][r]);
+                        D += xor1(D);  // the row-block's other half
+                    } else {
+                        const int4 lo = make_int4(w[u].x & 0x0F0F0F0F, w[u].y & 0x0F0F0F0F, w[u].z & 0x0F0F0F0F, w[u].w & 0x0F0F0F0F);
+                        const int4 hi = make_int4((w[u].x >> 4) & 0x0F0F0F0F, (w[u].y >> 4) & 0x0F0F0F0F,
+                                                  (w[u].z >> 4) & 0x0F0F0F0F, (w[u].w >> 4) & 0x0F0F0F0F);
+                        D = dot16(lo, a0[v][r]) + dot16(hi, a1[v][r]) + acr[v][r];
+                    }
+                    if (valid && h == 0) {
+                        if (OUT == OUT_DOTS) {
+                            const int n = (base + ql * qs) * 4 + L;
+                            p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * G + blk] = D;
+                        } else {
+                            const float scale = ws[u] * asc[v][r];
+                            terms[((tb * R + r) * NW + ql * 4 + L) * Gp + blk] = float(D) * scale;
+                        }
                     }
                 }
             }
@@ -412,11 +438,13 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     const int sub = int(threadIdx.x) - my_out * team;
     // the residual row this workgroup adds to, read early (linear.rs:139-142); read whether or not
     // it is added, so that no branch splits the loads before the weights' first batch
-    float resid = 0.0f;
-    if (OUT == OUT_STORE) {
+    float resid = 0.0f, bias0 = 0.0f;
+    if (OUT != OUT_SWIGLU && OUT != OUT_DOTS) {
         const int r = my_out / NW, nl = my_out - r * NW;
         const bool mine = r < R && nl < nq * 4;
-        resid = p.out[mine ? r * p.ld_out + (output_of(nl) - p.col_begin) : 0];
+        if (OUT == OUT_STORE) resid = p.out[mine ? r * p.ld_out + (output_of(nl) - p.col_begin) : 0];
+        // and the bias of that output (a table without bias reads its own scales instead, unused)
+        bias0 = (p.bias ? p.bias : p.wscales)[mine ? min(output_of(nl), p.n_rows - 1) : 0];
     }
     // keep the activation loads ahead of the weights': loads return in order, and the prologue
     // waits only for the activations
@@ -441,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         const int tb = i / (R * NW), rem = i - tb * R * NW;
         const int r = rem / NW, nl = rem - r * NW;
         const int n = output_of(nl);
-        if (OUT != OUT_SWIGLU && p.bias && n < p.n_rows) s = s + p.bias[n];
+        if (OUT != OUT_SWIGLU && p.bias && n < p.n_rows) s = s + (i == my_out ? bias0 : p.bias[n]);
         if (OUT == OUT_STORE) {
             float *o = p.out + r * p.ld_out + (n - p.col_begin);
             float prior = resid;
@@ -590,6 +618,40 @@ int dispatch_exact(const ProjParams &p, bool exact, size_t smem, unsigned grid, 
                  : launch_one<FMT, 1, IN, OUT, false, NB, true>(p, smem, grid, s);
 }
 
+// Batch depth: the fewest chunks in flight per wave (1, 2, 4 or 8) that cover a wave's share in
+// one batch. A wave's instructions are its latency at one wave per SIMD, so the address
+// arithmetic and reads of unused batch slots would cost time at small shares.
+int batch_depth(const ProjParams &p, int dtype, int out)
+{
+    const int qb_per_chunk = dtype == FG_Q4B32 ? 16 : 8;
+    const int per_table = (p.qpw * p.B + qb_per_chunk - 1) / qb_per_chunk;
+    const int stride = out == OUT_SWIGLU ? 2 : 4;
+    const int mine = (per_table + stride - 1) / stride;
+    return mine <= 1 ? 1 : mine <= 2 ? 2 : mine <= 4 ? 4 : 8;
+}
+
+template <int FMT, int IN, int OUT>
+int dispatch_depth(const ProjParams &p, bool exact, int depth, size_t smem, unsigned grid, hipStream_t s)
+{
+    switch (depth) {
+    case 1: return dispatch_exact<FMT, IN, OUT, 1>(p, exact, smem, grid, s);
+    case 2: return dispatch_exact<FMT, IN, OUT, 2>(p, exact, smem, grid, s);
+    case 4: return dispatch_exact<FMT, IN, OUT, 4>(p, exact, smem, grid, s);
+    default: return dispatch_exact<FMT, IN, OUT, 8>(p, exact, smem, grid, s);
+    }
+}
+
+template <int FMT>
+int dispatch_attn(const ProjParams &p, int depth, size_t smem, unsigned grid, hipStream_t s)
+{
+    switch (depth) {  // the merge is the parallel-order attention's
+    case 1: return launch_one<FMT, 1, IN_ATTN, OUT_STORE, false, 1, true>(p, smem, grid, s);
+    case 2: return launch_one<FMT, 1, IN_ATTN, OUT_STORE, false, 2, true>(p, smem, grid, s);
+    case 4: return launch_one<FMT, 1, IN_ATTN, OUT_STORE, false, 4, true>(p, smem, grid, s);
+    default: return launch_one<FMT, 1, IN_ATTN, OUT_STORE, false, 8, true>(p, smem, grid, s);
+    }
+}
+
 }  // namespace
 
 size_t proj_smem(const ProjParams &p, int rows, int in, int out)
@@ -614,25 +676,24 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     const size_t smem = proj_smem(p, 1, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
     const bool q4 = dtype == FG_Q4B32;
+    const int nb = batch_depth(p, dtype, out);
     switch (out) {
     case OUT_QKV:
-        return q4 ? dispatch_exact<4, IN_NORM, OUT_QKV, 8>(p, exact, smem, grid, s)
-                  : dispatch_exact<8, IN_NORM, OUT_QKV, 8>(p, exact, smem, grid, s);
+        return q4 ? dispatch_depth<4, IN_NORM, OUT_QKV>(p, exact, nb, smem, grid, s)
+                  : dispatch_depth<8, IN_NORM, OUT_QKV>(p, exact, nb, smem, grid, s);
     case OUT_SWIGLU:
-        return q4 ? dispatch_exact<4, IN_NORM, OUT_SWIGLU, 8>(p, exact, smem, grid, s)
-                  : dispatch_exact<8, IN_NORM, OUT_SWIGLU, 8>(p, exact, smem, grid, s);
+        return q4 ? dispatch_depth<4, IN_NORM, OUT_SWIGLU>(p, exact, nb, smem, grid, s)
+                  : dispatch_depth<8, IN_NORM, OUT_SWIGLU>(p, exact, nb, smem, grid, s);
     default:
         if (in == IN_NORM)
-            return q4 ? dispatch_exact<4, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s)
-                      : dispatch_exact<8, IN_NORM, OUT_STORE, 8>(p, exact, smem, grid, s);
+            return q4 ? dispatch_depth<4, IN_NORM, OUT_STORE>(p, exact, nb, smem, grid, s)
+                      : dispatch_depth<8, IN_NORM, OUT_STORE>(p, exact, nb, smem, grid, s);
         if (in == IN_F32)
-            return q4 ? dispatch_exact<4, IN_F32, OUT_STORE, 8>(p, exact, smem, grid, s)
-                      : dispatch_exact<8, IN_F32, OUT_STORE, 8>(p, exact, smem, grid, s);
-        if (in == IN_ATTN)  // the merge is the parallel-order attention's
-            return q4 ? launch_one<4, 1, IN_ATTN, OUT_STORE, false, 8, true>(p, smem, grid, s)
-                      : launch_one<8, 1, IN_ATTN, OUT_STORE, false, 8, true>(p, smem, grid, s);
-        return q4 ? dispatch_exact<4, IN_PREQ, OUT_STORE, 8>(p, exact, smem, grid, s)
-                  : dispatch_exact<8, IN_PREQ, OUT_STORE, 8>(p, exact, smem, grid, s);
+            return q4 ? dispatch_depth<4, IN_F32, OUT_STORE>(p, exact, nb, smem, grid, s)
+                      : dispatch_depth<8, IN_F32, OUT_STORE>(p, exact, nb, smem, grid, s);
+        if (in == IN_ATTN) return q4 ? dispatch_attn<4>(p, nb, smem, grid, s) : dispatch_attn<8>(p, nb, smem, grid, s);
+        return q4 ? dispatch_depth<4, IN_PREQ, OUT_STORE>(p, exact, nb, smem, grid, s)
+                  : dispatch_depth<8, IN_PREQ, OUT_STORE>(p, exact, nb, smem, grid, s);
     }
 }
 

@@ -244,8 +244,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
         }
         float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
         amax = max8(fmaxf(0.0f, amax));
-        const float d = group_scale(amax, 127.0f);
-        const int l0 = quantize_level(x[0], d), l1 = quantize_level(x[1], d), l2 = quantize_level(x[2], d), l3 = quantize_level(x[3], d);
+        int l0, l1, l2, l3;
+        const float d = scale_and_levels(amax, x[0], x[1], x[2], x[3], l0, l1, l2, l3);
         const int sum = sum8(l0 + l1 + l2 + l3);
         const int G = (head * D + d0) / 32;
         reinterpret_cast<int *>(a.q)[G * 8 + sub] = pack4(l0, l1, l2, l3);

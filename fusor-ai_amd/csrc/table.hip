@@ -170,8 +170,8 @@ __global__ void quantize_rows_kernel(const float *__restrict__ x, size_t groups,
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = max8(fmaxf(0.0f, amax));
     for (int m = 8; m < LANES; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
-    float d = group_scale(amax, 127.0f);
-    int l0 = quantize_level(v.x, d), l1 = quantize_level(v.y, d), l2 = quantize_level(v.z, d), l3 = quantize_level(v.w, d);
+    int l0, l1, l2, l3;
+    const float d = scale_and_levels(amax, v.x, v.y, v.z, v.w, l0, l1, l2, l3);
     int sum = sum8(l0 + l1 + l2 + l3);
     for (int m = 8; m < LANES; m <<= 1) sum += __shfl_xor(sum, m, 64);
     if (!active) return;

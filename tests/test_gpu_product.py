@@ -120,6 +120,45 @@ def test_quantize_rows_matches_the_oracle(fk, dtype, count):
     assert np.array_equal(host(c), wc)
 
 
+def near_ties(groups, seed):
+    """Groups whose largest magnitude spans every binade (subnormal to near the largest float) and
+    whose other values sit at and within a few ulps of the half-integer multiples of the group's
+    scale d = amax / 127, where the rounding of the quotient decides the level."""
+    rng = np.random.default_rng(seed)
+    exps = rng.integers(-149, 128, groups)
+    amax = (rng.uniform(1.0, 2.0, groups) * np.exp2(exps.astype(np.float64))).astype(np.float32)
+    amax[amax == 0] = np.float32(1e-45)
+    amax[~np.isfinite(amax)] = np.float32(3e38)
+    d = amax / np.float32(127.0)
+    k = rng.integers(-127, 127, (groups, 32)).astype(np.float32)
+    x = ((k + np.float32(0.5)) * d[:, None]).astype(np.float32)
+    nudge = rng.integers(-3, 4, (groups, 32)).astype(np.int32)
+    mag = np.maximum(np.abs(x).view(np.int32) + nudge, 0).view(np.float32)
+    x = np.where(x < 0, -mag, mag).astype(np.float32)
+    x = np.clip(x, -amax[:, None], amax[:, None])
+    x[:, 0] = amax * np.where(rng.random(groups) < 0.5, 1, -1).astype(np.float32)
+    return x.reshape(-1)
+
+
+@pytest.mark.parametrize("dtype", [O.Q8B32, O.T2B128])
+def test_quantize_rows_rounds_quotients_at_every_scale(fk, dtype):
+    """Every level is the tie-to-even rounding of the IEEE quotient x / d, for scales from
+    subnormal to huge: the shared-reciprocal quotient and the division agree to the bit."""
+    import torch
+    x = near_ties(8192, seed=dtype)
+    count = x.size
+    g = O.group(dtype)
+    q = torch.empty(count, dtype=torch.int8, device="cuda")
+    s = torch.empty(count // g, dtype=torch.float32, device="cuda")
+    c = torch.empty(count // g, dtype=torch.int32, device="cuda")
+    fk.quantize_rows(dev(x), fk.QuantFormat(dtype), q, s, c)
+    wq, ws, wc = O.quantize_rows(x, dtype)
+    got = host(q)
+    assert np.array_equal(got, wq), np.flatnonzero(got != wq)[:8]
+    assert same_bits(host(s), ws)
+    assert np.array_equal(host(c), wc)
+
+
 # ------------------------------------------------------------------------------ products
 
 def gpu_product(fk, t, x, rows, cols=None, fused=True, bias=None, dots=False):

@@ -95,6 +95,7 @@ struct StageRegs {
     v4f pa[kMaxChunks];  // IN_ATTN: this lane's four sums of every chunk, and the chunks' max and total
     float pm[kMaxChunks], pl[kMaxChunks];
     v4f w0, w1, w2, w3;  // the RMSNorm weight (IN_NORM)
+    v4f qn, kn, vn;      // IN_ATTN: this lane's four dims of the rotated query, new key and new value
 };
 
 
@@ -106,33 +107,37 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
     if (IN == IN_PREQ) {
         const v4i *src = reinterpret_cast<const v4i *>(p.q);
         const int n16 = R * K / 16, ng = R * G;
-        g.v0 = src[min(tid, n16 - 1)];
-        g.v1 = src[min(tid + kThreads, n16 - 1)];
-        g.v2 = src[min(tid + 2 * kThreads, n16 - 1)];
-        g.v3 = src[min(tid + 3 * kThreads, n16 - 1)];
-        g.s0 = p.as[min(tid, ng - 1)];
-        g.s1 = p.as[min(tid + kThreads, ng - 1)];
-        g.s2 = p.as[min(tid + 2 * kThreads, ng - 1)];
-        g.s3 = p.as[min(tid + 3 * kThreads, ng - 1)];
-        g.c0 = p.corr[min(tid, ng - 1)];
-        g.c1 = p.corr[min(tid + kThreads, ng - 1)];
-        g.c2 = p.corr[min(tid + 2 * kThreads, ng - 1)];
-        g.c3 = p.corr[min(tid + 3 * kThreads, ng - 1)];
+        g.v0 = src[unsigned(min(tid, n16 - 1))];
+        g.v1 = src[unsigned(min(tid + kThreads, n16 - 1))];
+        g.v2 = src[unsigned(min(tid + 2 * kThreads, n16 - 1))];
+        g.v3 = src[unsigned(min(tid + 3 * kThreads, n16 - 1))];
+        g.s0 = p.as[unsigned(min(tid, ng - 1))];
+        g.s1 = p.as[unsigned(min(tid + kThreads, ng - 1))];
+        g.s2 = p.as[unsigned(min(tid + 2 * kThreads, ng - 1))];
+        g.s3 = p.as[unsigned(min(tid + 3 * kThreads, ng - 1))];
+        g.c0 = p.corr[unsigned(min(tid, ng - 1))];
+        g.c1 = p.corr[unsigned(min(tid + kThreads, ng - 1))];
+        g.c2 = p.corr[unsigned(min(tid + 2 * kThreads, ng - 1))];
+        g.c3 = p.corr[unsigned(min(tid + 3 * kThreads, ng - 1))];
     } else if (IN == IN_F32) {
         const v4f *x4 = reinterpret_cast<const v4f *>(p.x);
         const int n4 = R * K / 4;
-        g.f0 = x4[min(tid, n4 - 1)];
-        g.f1 = x4[min(tid + kThreads, n4 - 1)];
-        g.f2 = x4[min(tid + 2 * kThreads, n4 - 1)];
-        g.f3 = x4[min(tid + 3 * kThreads, n4 - 1)];
-        g.f4 = x4[min(tid + 4 * kThreads, n4 - 1)];
-        g.f5 = x4[min(tid + 5 * kThreads, n4 - 1)];
-        g.f6 = x4[min(tid + 6 * kThreads, n4 - 1)];
-        g.f7 = x4[min(tid + 7 * kThreads, n4 - 1)];
+        g.f0 = x4[unsigned(min(tid, n4 - 1))];
+        g.f1 = x4[unsigned(min(tid + kThreads, n4 - 1))];
+        g.f2 = x4[unsigned(min(tid + 2 * kThreads, n4 - 1))];
+        g.f3 = x4[unsigned(min(tid + 3 * kThreads, n4 - 1))];
+        g.f4 = x4[unsigned(min(tid + 4 * kThreads, n4 - 1))];
+        g.f5 = x4[unsigned(min(tid + 5 * kThreads, n4 - 1))];
+        g.f6 = x4[unsigned(min(tid + 6 * kThreads, n4 - 1))];
+        g.f7 = x4[unsigned(min(tid + 7 * kThreads, n4 - 1))];
     } else if (IN == IN_ATTN) {
         // lane t merges float4 t of the attention row (head t·4 / D); every chunk's record at once
         const int e = min(tid, K / 4 - 1);
         const int h = e * 4 / p.D, d4 = e * 4 - h * p.D;
+        const size_t at = p.layer_base + (size_t(h / (p.heads / p.kv_heads)) * p.capacity + size_t(p.position)) * p.D + d4;
+        g.qn = *reinterpret_cast<const v4f *>(p.qkv_out + size_t(h) * p.D + d4);
+        g.kn = *reinterpret_cast<const v4f *>(p.kcache + at);
+        g.vn = *reinterpret_cast<const v4f *>(p.vcache + at);
 #pragma unroll
         for (int c = 0; c < kMaxChunks; c++) {
             const float *rec = p.part + size_t(h * p.chunks + min(c, p.chunks - 1)) * (p.D + 4);
@@ -145,14 +150,14 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
         const v4f *x4 = reinterpret_cast<const v4f *>(p.x);
         const v4f *w4 = reinterpret_cast<const v4f *>(p.norm_w);
         const int n4 = K / 4;
-        g.f0 = x4[min(tid, n4 - 1)];
-        g.f1 = x4[min(tid + kThreads, n4 - 1)];
-        g.f2 = x4[min(tid + 2 * kThreads, n4 - 1)];
-        g.f3 = x4[min(tid + 3 * kThreads, n4 - 1)];
-        g.w0 = w4[min(tid, n4 - 1)];
-        g.w1 = w4[min(tid + kThreads, n4 - 1)];
-        g.w2 = w4[min(tid + 2 * kThreads, n4 - 1)];
-        g.w3 = w4[min(tid + 3 * kThreads, n4 - 1)];
+        g.f0 = x4[unsigned(min(tid, n4 - 1))];
+        g.f1 = x4[unsigned(min(tid + kThreads, n4 - 1))];
+        g.f2 = x4[unsigned(min(tid + 2 * kThreads, n4 - 1))];
+        g.f3 = x4[unsigned(min(tid + 3 * kThreads, n4 - 1))];
+        g.w0 = w4[unsigned(min(tid, n4 - 1))];
+        g.w1 = w4[unsigned(min(tid + kThreads, n4 - 1))];
+        g.w2 = w4[unsigned(min(tid + 2 * kThreads, n4 - 1))];
+        g.w3 = w4[unsigned(min(tid + 3 * kThreads, n4 - 1))];
     }
 }
 
@@ -221,14 +226,24 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             if (tid + i0 < n4) store_group8(gr[0], p.zp, i / 8, act_q, act_s, act_c);
         }
     } else if (IN == IN_ATTN) {
-        // the chunks' softmax states merged (flash decoding): M = max m_c, L = Σ l_c·e^(m_c − M),
-        // out = Σ acc_c·e^(m_c − M) / L; then the row quantized (8 lanes per group of 32)
-        float M = g.pm[0];
+        // the chunks' softmax states and the new key's (score s_n = q·k_n/√D, total 1, sums v_n)
+        // merged (flash decoding): M = max(s_n, m_c), L = e^(s_n − M) + Σ l_c·e^(m_c − M),
+        // out = (v_n·e^(s_n − M) + Σ acc_c·e^(m_c − M)) / L; then the row quantized (8 lanes per
+        // group of 32). The head's D / 4 lanes are aligned, so its dot product is a group sum.
+        const v4f qk = g.qn * g.kn;
+        float sn = (qk.x + qk.y) + (qk.z + qk.w);
+        sn = sn + __int_as_float(xor1(__float_as_int(sn)));
+        sn = sn + __int_as_float(xor2(__float_as_int(sn)));
+        sn = sn + __int_as_float(mirror8(__float_as_int(sn)));
+        for (int w = 8; w < p.D / 4; w <<= 1) sn = sn + __shfl_xor(sn, w, 64);
+        sn = sn * (1.0f / sqrtf(float(p.D)));
+        float M = sn;
 #pragma unroll
-        for (int c = 1; c < kMaxChunks; c++)
+        for (int c = 0; c < kMaxChunks; c++)
             if (c < p.chunks) M = fmaxf(M, g.pm[c]);
-        float L = 0.0f;
-        v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float en = ref_exp(sn - M);
+        float L = en;
+        v4f o = g.vn * en;
 #pragma unroll
         for (int c = 0; c < kMaxChunks; c++) {
             if (c < p.chunks) {
@@ -290,20 +305,144 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
     }
 }
 
+// ---------------------------------------------------------------- the fast attention's chunks
+//
+// One query head over one chunk of the cached keys (flash decoding), 256 threads. Per tile of
+// kTileKeys keys: the scores q·k_j·(1/√D) (ops.rs:310-326; four lanes per key), the running maximum
+// m, e^(s_j − m) through ops::exp, the running total l and the running weighted sum of values
+// (ops.rs:329-342), both rescaled by e^(m_old − m) when the maximum moves. The chunk's record is
+// (m, l, −, −, acc[D]); the output projection's prologue merges the records with the new key's.
+
+// A tile's keys and values as one thread holds them: for the scores, key jk = t / 4, dims
+// (t % 4)·D/4 ..; for the weighted sum, dim t % D of keys t / D, t / D + 256 / D, ...
+template <int D>
+struct KVTile {
+    v4f k[D >= 16 ? D / 16 : 1];
+    float v[D >= 4 ? D / 4 : 1];
+};
+
+// The tile of keys j0 .. j0 + n - 1 of KV head `kv` (branch-free: keys past n re-read key j0).
+template <int D>
+__device__ __forceinline__ void load_kv_tile(const ProjParams &p, int kv, int j0, int n, KVTile<D> &t)
+{
+    if (D == 0) return;
+    constexpr int DQ = D / 4, KG = kThreads / (D > 0 ? D : 1), VK = kTileKeys / (KG > 0 ? KG : 1);
+    const int tid = threadIdx.x, jk = tid >> 2, part = tid & 3, d = tid % (D > 0 ? D : 1), g = tid / (D > 0 ? D : 1);
+    const size_t row0 = p.layer_base + (size_t(kv) * p.capacity + size_t(j0)) * D;  // the tile's first key
+    const float *kt = p.kcache + row0, *vt = p.vcache + row0;
+    const unsigned koff = unsigned((jk < n ? jk : 0) * D + part * DQ);
+#pragma unroll
+    for (int i = 0; i < DQ / 4; i++) t.k[i] = *reinterpret_cast<const v4f *>(kt + (koff + 4u * i));
+#pragma unroll
+    for (int e = 0; e < VK; e++) {
+        const int j = g + e * KG;
+        t.v[e] = vt[unsigned((j < n ? j : 0) * D + d)];
+    }
+}
+
+// Chunk c of query head h: keys [c·per_chunk, min((c + 1)·per_chunk, position)); the first tile is
+// already in `tile`. `scratch` holds kTileKeys + 8 + 256 floats of LDS.
+template <int D>
+__device__ __forceinline__ void attend_chunk(const ProjParams &p, const float *qrot, int h, int c, KVTile<D> &tile,
+                                             float *scratch)
+{
+    if (D == 0) return;
+    constexpr int DQ = D / 4, KG = kThreads / (D > 0 ? D : 1), VK = kTileKeys / (KG > 0 ? KG : 1);
+    float *pw = scratch;            // [kTileKeys] the tile's weights
+    float *red = pw + kTileKeys;    // [8] per-wave maxima and totals
+    float *sums = red + 8;          // [256] the weighted sums' partials
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int jk = tid >> 2, part = tid & 3, d = tid % (D > 0 ? D : 1), g = tid / (D > 0 ? D : 1);
+    const int kv = h / (p.heads / p.kv_heads);
+    const int first = c * p.per_chunk, last = min(p.position, first + p.per_chunk);
+    v4f q[DQ / 4 > 0 ? DQ / 4 : 1];
+#pragma unroll
+    for (int i = 0; i < DQ / 4; i++) q[i] = *reinterpret_cast<const v4f *>(qrot + part * DQ + 4 * i);
+    const float scale = 1.0f / sqrtf(float(D));
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int j0 = first; j0 < last; j0 += kTileKeys) {
+        const int n = min(kTileKeys, last - j0);
+        if (j0 != first) load_kv_tile<D>(p, kv, j0, n, tile);
+        v4f sv = q[0] * tile.k[0];
+#pragma unroll
+        for (int i = 1; i < DQ / 4; i++) sv = sv + q[i] * tile.k[i];
+        float sc = (sv.x + sv.y) + (sv.z + sv.w);
+        sc = sc + __int_as_float(xor1(__float_as_int(sc)));
+        sc = sc + __int_as_float(xor2(__float_as_int(sc)));
+        sc = jk < n ? sc * scale : -INFINITY;
+        const float wm = wave_max(sc);
+        if (lane == 0) red[wave] = wm;
+        __syncthreads();
+        const float m_new = fmaxf(m, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        const float r = m == -INFINITY ? 0.0f : ref_exp(m - m_new);
+        const float pj = jk < n ? ref_exp(sc - m_new) : 0.0f;
+        const float ws = wave_sum_unordered(part == 0 ? pj : 0.0f);
+        if (part == 0) pw[jk] = pj;
+        if (lane == 0) red[4 + wave] = ws;
+        __syncthreads();
+        l = l * r + ((red[4] + red[5]) + (red[6] + red[7]));
+        m = m_new;
+        acc = acc * r;
+#pragma unroll
+        for (int e = 0; e < VK; e++) {
+            const int j = g + e * KG;
+            acc = acc + (j < n ? pw[j] * tile.v[e] : 0.0f);
+        }
+        __syncthreads();  // pw and red are the next tile's
+    }
+    sums[tid] = acc;
+    __syncthreads();
+    float *rec = p.states + size_t(h * p.chunks + c) * (D + 4);
+    if (g == 0) {
+        float o = acc;
+#pragma unroll
+        for (int gg = 1; gg < KG; gg++) o = o + sums[gg * D + d];
+        rec[4 + d] = o;
+    }
+    if (tid == 0) {
+        rec[0] = m;
+        rec[1] = l;
+    }
+}
+
+// The (head, chunk) unit, head·chunks + chunk, of query workgroup w. Workgroups go to the eight
+// XCDs in turn (w % 8), so consecutive units are spread over w = x, x + 8, ... of one XCD: the
+// chunk workgroups of a head then share that XCD's L2 for the head's rows.
+__device__ __forceinline__ int qattn_unit(const ProjParams &p, int w, int qwgs)
+{
+    return qwgs % 8 ? w : (w % 8) * (qwgs / 8) + w / 8;
+}
+
 // FMT: 8 for signed 8-bit levels (Q7b32 folded, Q8b32), 4 for offset nibbles (Q4b32).
 // TREE: each output's group terms summed by a team of lanes and a lane reduction instead of in
 // group order (the decoder's parallel-order mode; the product's own entry points never use it).
-template <int FMT, int R, int IN, int OUT, bool EXACT, int kBatch, bool TREE>
+template <int FMT, int R, int IN, int OUT, bool EXACT, int kBatch, bool TREE, int HD>
 __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
 {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int NT = OUT == OUT_SWIGLU ? 2 : 1;  // tables streamed
     const int K = p.K, G = p.G, B = p.B;
     const int Gp = (G + 3) & ~3;  // terms per output, padded for 128-bit reads
-    const int qs = p.qstride;
-    const int base = p.quad_begin + int(blockIdx.x) / qs * qs * p.qpw + int(blockIdx.x) % qs;
-    const int nq = base < p.quad_end ? min(p.qpw, (p.quad_end - base + qs - 1) / qs) : 0;
-    if (nq <= 0) return;  // the host's grids leave none empty
+    // OUT_QATTN: the query workgroups own their head's D/4 quads, the others a rotary pair of the
+    // key and value rows (quads D/8 apart). Branch-free, so that the parameters' loads issue at once.
+    const int w = int(blockIdx.x);
+    const int qwgs = OUT == OUT_QATTN ? p.heads * p.chunks : 0;
+    const bool query = OUT == OUT_QATTN && w < qwgs;
+    int qs, base, nq;
+    if (OUT == OUT_QATTN) {
+        constexpr int hq = HD / 8;
+        const int b = w - qwgs;
+        qs = query ? 1 : hq;
+        base = query ? qattn_unit(p, w, qwgs) / p.chunks * (HD / 4) : p.heads * (HD / 4) + b / hq * hq * 2 + b % hq;
+        nq = query ? HD / 4 : 2;
+    } else {
+        qs = p.qstride;
+        base = p.quad_begin + ((w >> p.qshift) << p.qshift) * p.qpw + (w & (qs - 1));
+        nq = min(p.qpw, (p.quad_end - base + qs - 1) >> p.qshift);
+    }
+    // The host's grids leave no workgroup without quads. No early exit (it would put a round trip
+    // for the parameters ahead of every load): the clamp only keeps any access in bounds.
+    nq = max(nq, 1);
     const int NW = p.qpw * 4;
     auto output_of = [&](int nl) { return (base + (nl >> 2) * qs) * 4 + (nl & 3); };  // local -> column
     const ProjLayout lay = proj_layout(R, K, G, NW, IN, OUT);
@@ -348,26 +487,34 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             cu.ql++;
         }
     };
-    Cursor lcur{qb0 / B, qb0 % B};
-    Cursor ccur = lcur;
+    Cursor ccur{qb0 / B, qb0 % B};
 
-    // Branch-free: every lane loads, past the run's end from its last quad (always in bounds), so
-    // the loads of a batch issue back to back with a single wait when consumed; `consume` skips
-    // what was not valid. The cursor keeps blk < B, so only the quad needs the clamp.
+    // The workgroup's quad blocks, numbered ql·B + blk, sit contiguously from its first quad, but
+    // for a strided pair (qs > 1, two quads) whose second half starts (qs − 1)·B blocks later.
+    // Lanes address them as 32-bit offsets from the workgroup's base (the loads' scalar-base form),
+    // a few instructions per chunk. Branch-free: past the run's end every lane reloads the last
+    // block (always in bounds), so a batch issues back to back with a single wait when consumed;
+    // `consume` skips what was not valid.
+    const int8_t *wq = codes + size_t(base) * B * QB;
+    const float *sq = wsc + size_t(base) * G * 4;
+    const unsigned skip = unsigned(qs - 1) * unsigned(B), last_qb = unsigned(nq * B - 1);
+    unsigned lqb = unsigned(qb0);
     auto load = [&](int4 *w, float *ws) {
 #pragma unroll
         for (int u = 0; u < kBatch; u++) {
-            const size_t quad = size_t(base + min(lcur.ql, nq - 1) * qs);
-            w[u] = *reinterpret_cast<const int4 *>(codes + (quad * B + lcur.blk) * QB + piece * 16);
-            ws[u] = wsc[(quad * G + lcur.blk) * 4 + L];
-            advance(lcur);
+            const unsigned qb = min(lqb, last_qb);
+            const unsigned at = qb + (qb >= unsigned(B) ? skip : 0u);
+            w[u] = *reinterpret_cast<const int4 *>(wq + (at * QB + unsigned(piece) * 16u));
+            ws[u] = sq[at * 4u + unsigned(L)];
+            lqb += unsigned(stride * QB_PER_CHUNK);
         }
     };
 
     // A batch is consumed U chunks at a time: the chunks' activation reads from LDS first, then
     // their dots and term stores. LDS reads are not moved above possibly aliasing LDS stores, so
     // reading per chunk would serialize two LDS round trips per chunk.
-    constexpr int U = R == 1 ? (FMT == 8 ? kBatch : (kBatch + 1) / 2) : (R == 2 ? (kBatch < 4 ? kBatch : 4) : (kBatch < 2 ? kBatch : 2));
+    constexpr int U = R == 1 ? (FMT == 8 ? (kBatch < 8 ? kBatch : 8) : (kBatch < 8 ? (kBatch + 1) / 2 : 4))
+                             : (R == 2 ? (kBatch < 4 ? kBatch : 4) : (kBatch < 2 ? kBatch : 2));
     auto consume = [&](int b, const int4 *w, const float *ws) {
 #pragma unroll
         for (int u0 = 0; u0 < kBatch; u0 += U) {
@@ -425,40 +572,65 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         }
     };
 
-    int4 wa[kBatch], wb[kBatch];
-    float sa[kBatch], sb[kBatch];
+    // Batches of up to 8 chunks are double-buffered (the next batch in flight while one is
+    // consumed); a deeper batch, sized to cover a wave's whole share, has a single buffer.
+    constexpr bool kDouble = kBatch <= 8;
+    constexpr int kSecond = kDouble ? kBatch : 1;
+    int4 wa[kBatch], wb[kSecond];
+    float sa[kBatch], sb[kSecond];
     StageRegs g;
     stage_issue<R, IN>(p, g);
     // Who sums which output: one thread per output, or (TREE) a team of `team` lanes per output.
     const int outs = NT * R * NW;
-    int team = 1;
-    if (TREE)
-        while (team < 64 && outs * team * 2 <= kThreads) team <<= 1;
-    const int my_out = TREE ? int(threadIdx.x) / team : int(threadIdx.x);
+    // the largest power of two (at most 64) with outs·team <= 256: no loop ahead of the loads
+    const int team = TREE ? min(64, int(0x80000000u >> __builtin_clz(unsigned(max(1, kThreads / outs))))) : 1;
+    const int my_out = TREE ? int(threadIdx.x) >> __builtin_ctz(unsigned(team)) : int(threadIdx.x);
     const int sub = int(threadIdx.x) - my_out * team;
     // the residual row this workgroup adds to, read early (linear.rs:139-142); read whether or not
     // it is added, so that no branch splits the loads before the weights' first batch
     float resid = 0.0f, bias0 = 0.0f;
     if (OUT != OUT_SWIGLU && OUT != OUT_DOTS) {
-        const int r = my_out / NW, nl = my_out - r * NW;
+        const int r = R == 1 ? 0 : my_out / NW, nl = my_out - r * NW;
         const bool mine = r < R && nl < nq * 4;
-        if (OUT == OUT_STORE) resid = p.out[mine ? r * p.ld_out + (output_of(nl) - p.col_begin) : 0];
+        const int n = output_of(nl);
+        // 32-bit offsets, selected rather than branched on, so no branch splits the loads
+        const unsigned at = unsigned(r) * unsigned(p.ld_out) + unsigned(n - p.col_begin);
+        if (OUT == OUT_STORE) resid = p.out[mine ? at : 0u];
         // and the bias of that output (a table without bias reads its own scales instead, unused)
-        bias0 = (p.bias ? p.bias : p.wscales)[mine ? min(output_of(nl), p.n_rows - 1) : 0];
+        bias0 = (p.bias ? p.bias : p.wscales)[mine ? unsigned(min(n, p.n_rows - 1)) : 0u];
     }
     // keep the activation loads ahead of the weights': loads return in order, and the prologue
     // waits only for the activations
     __builtin_amdgcn_sched_barrier(0);
     load(wa, sa);  // every wave, in bounds even without chunks of its own
     __builtin_amdgcn_sched_barrier(0);  // and all of them issued before the prologue's first wait
+    // OUT_QATTN: the first tile of the chunk's cached keys and values, behind the weights (every
+    // workgroup loads one, in bounds, so that no branch splits the loads)
+    KVTile<HD> tile;
+    int head = 0, chunk = 0;
+    if (OUT == OUT_QATTN) {
+        const int unit = query ? qattn_unit(p, int(blockIdx.x), qwgs) : 0;
+        head = unit / p.chunks;
+        chunk = unit % p.chunks;
+        const int first = chunk * p.per_chunk;
+        load_kv_tile<HD>(p, head / (p.heads / p.kv_heads), first, max(0, min(kTileKeys, min(p.position, first + p.per_chunk) - first)), tile);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
     __syncthreads();
-    for (int b = 0; b < batches; b += 2) {
-        if (b + 1 < batches) load(wb, sb);
-        consume(b, wa, sa);
-        if (b + 1 < batches) {
-            if (b + 2 < batches) load(wa, sa);
-            consume(b + 1, wb, sb);
+    if constexpr (kDouble) {
+        for (int b = 0; b < batches; b += 2) {
+            if (b + 1 < batches) load(wb, sb);
+            consume(b, wa, sa);
+            if (b + 1 < batches) {
+                if (b + 2 < batches) load(wa, sa);
+                consume(b + 1, wb, sb);
+            }
+        }
+    } else {
+        for (int b = 0; b < batches; b++) {
+            if (b > 0) load(wa, sa);
+            consume(b, wa, sa);
         }
     }
     if (OUT == OUT_DOTS) return;
@@ -540,7 +712,26 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         return;
     }
     __syncthreads();
-    if (OUT == OUT_QKV) {
+    if (OUT == OUT_QATTN && query) {
+        // the query head: rotated by halves (rope_half, ops.rs:77-85), kept for the output
+        // projection's new-key term by the chunk-0 workgroup, then attended over the chunk
+        float *qrot = reinterpret_cast<float *>(smem + lay.off_att);
+        constexpr int half = HD / 2;
+        if (threadIdx.x < half) {
+            const int j = int(threadIdx.x);
+            const float x = ybuf[j] , y = ybuf[half + j];
+            const float c = p.rope[j], sn = p.rope[half + j];
+            const float nx = x * c - y * sn, ny = y * c + x * sn;
+            qrot[j] = nx;
+            qrot[j + half] = ny;
+            if (chunk == 0) {
+                p.qkv_out[head * HD + j] = nx;
+                p.qkv_out[head * HD + j + half] = ny;
+            }
+        }
+        __syncthreads();
+        attend_chunk<HD>(p, qrot, head, chunk, tile, qrot + HD);
+    } else if (OUT == OUT_QKV || OUT == OUT_QATTN) {
         // a rotary pair per workgroup (qstride = D/8, qpw = 2): outputs 0..3 are dimensions
         // j0..j0+3 of a head, outputs 4..7 the same dimensions + D/2. The bias is in; query and key
         // heads rotate by halves, key and value heads go to the cache.
@@ -573,10 +764,10 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     }
 }
 
-template <int FMT, int R, int IN, int OUT, bool EXACT, int NB = 8, bool TREE = false>
+template <int FMT, int R, int IN, int OUT, bool EXACT, int NB = 8, bool TREE = false, int HD = 0>
 int launch_one(const ProjParams &p, size_t smem, unsigned grid, hipStream_t s)
 {
-    auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT, NB, TREE>;
+    auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT, NB, TREE, HD>;
     if (smem > 64 * 1024) {
         static bool raised = false;
         if (!raised) {
@@ -641,6 +832,24 @@ int dispatch_depth(const ProjParams &p, bool exact, int depth, size_t smem, unsi
     }
 }
 
+// The query workgroups stream a whole head (D rows): one batch of up to 16 chunks per wave.
+template <int FMT, int HD>
+int dispatch_qattn_depth(const ProjParams &p, int depth, size_t smem, unsigned grid, hipStream_t s)
+{
+    return depth <= 1 ? launch_one<FMT, 1, IN_NORM, OUT_QATTN, false, 1, true, HD>(p, smem, grid, s)
+                      : launch_one<FMT, 1, IN_NORM, OUT_QATTN, false, 16, true, HD>(p, smem, grid, s);
+}
+
+template <int FMT>
+int dispatch_qattn(const ProjParams &p, int depth, size_t smem, unsigned grid, hipStream_t s)
+{
+    switch (p.D) {
+    case 32: return dispatch_qattn_depth<FMT, 32>(p, depth, smem, grid, s);
+    case 64: return dispatch_qattn_depth<FMT, 64>(p, depth, smem, grid, s);
+    default: return dispatch_qattn_depth<FMT, 128>(p, depth, smem, grid, s);
+    }
+}
+
 template <int FMT>
 int dispatch_attn(const ProjParams &p, int depth, size_t smem, unsigned grid, hipStream_t s)
 {
@@ -665,14 +874,24 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     const int nq = p.quad_end - p.quad_begin;
     if (nq <= 0) return FG_OK;
     if (p.qstride < 1) p.qstride = 1;
+    if (p.qstride & (p.qstride - 1)) return set_error(FG_ERR_SHAPE, "the quad stride is a power of two");
+    p.qshift = __builtin_ctz(unsigned(p.qstride));
     const int span = p.qstride * p.qpw;
-    if (p.qstride > 1 && nq % span) return set_error(FG_ERR_SHAPE, "strided quads cover whole spans");
+    if (p.qstride > 1 && (nq % span || p.qpw != 2)) return set_error(FG_ERR_SHAPE, "strided quads come in whole pairs");
     if (out == OUT_QKV && (p.qpw != 2 || p.qstride * 8 != p.D))
         return set_error(FG_ERR_SHAPE, "the QKV epilogue takes one rotary pair per workgroup");
     if (in == IN_NORM && p.K > 4 * 4 * kThreads) return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
-    if (in == IN_ATTN && (p.K > 4 * kThreads || p.chunks < 1 || p.chunks > kMaxChunks || p.heads * p.D != p.K))
-        return set_error(FG_ERR_SHAPE, "the attention merge takes rows of at most 1024 and 1 to 8 chunks");
-    const unsigned grid = p.qstride == 1 ? unsigned((nq + p.qpw - 1) / p.qpw) : unsigned(nq / span * p.qstride);
+    if (in == IN_ATTN && (p.K > 4 * kThreads || p.chunks < 1 || p.chunks > kMaxChunks || p.heads * p.D != p.K ||
+                          (p.D != 32 && p.D != 64 && p.D != 128) || p.kv_heads < 1 || p.heads % p.kv_heads))
+        return set_error(FG_ERR_SHAPE, "the attention merge takes rows of at most 1024, head_dim 32/64/128 and 1 to 8 chunks");
+    if (out == OUT_QATTN &&
+        ((p.D != 32 && p.D != 64 && p.D != 128) || p.qpw * 4 != p.D || p.qstride != 1 || p.kv_heads < 1 || p.heads % p.kv_heads ||
+         (p.heads + 2 * p.kv_heads) * p.D != p.n_rows || p.n_rows % 4 || p.chunks < 1 || p.chunks > kMaxChunks ||
+         p.per_chunk < kTileKeys || size_t(p.chunks) * p.per_chunk < size_t(p.position) || p.position >= p.capacity))
+        return set_error(FG_ERR_SHAPE, "the query attention takes head_dim 32/64/128, whole query and key heads and 1 to 8 chunks");
+    const unsigned grid = out == OUT_QATTN ? unsigned(p.heads * p.chunks + 2 * p.kv_heads * (p.D / 8))
+                          : p.qstride == 1 ? unsigned((nq + p.qpw - 1) / p.qpw)
+                                           : unsigned(nq / span * p.qstride);
     const size_t smem = proj_smem(p, 1, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
     const bool q4 = dtype == FG_Q4B32;
@@ -684,6 +903,9 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     case OUT_SWIGLU:
         return q4 ? dispatch_depth<4, IN_NORM, OUT_SWIGLU>(p, exact, nb, smem, grid, s)
                   : dispatch_depth<8, IN_NORM, OUT_SWIGLU>(p, exact, nb, smem, grid, s);
+    case OUT_QATTN:  // the parallel-order attention's
+        if (in != IN_NORM || exact) return set_error(FG_ERR_SHAPE, "the query attention takes a normed row in parallel order");
+        return q4 ? dispatch_qattn<4>(p, nb, smem, grid, s) : dispatch_qattn<8>(p, nb, smem, grid, s);
     default:
         if (in == IN_NORM)
             return q4 ? dispatch_depth<4, IN_NORM, OUT_STORE>(p, exact, nb, smem, grid, s)

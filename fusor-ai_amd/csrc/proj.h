@@ -12,9 +12,11 @@ namespace fg {
 constexpr int IN_PREQ = 0, IN_F32 = 1, IN_NORM = 2, IN_ATTN = 3;
 // Chunks of keys per query head in the fast attention; the output projection merges them.
 constexpr int kMaxChunks = 8;
+constexpr int kTileKeys = 64;  // keys per tile of the fast attention
 // Output: store (bias / residual / greedy candidates), the int32 group accumulators, the QKV
-// epilogue, the gated feed-forward epilogue.
-constexpr int OUT_STORE = 0, OUT_DOTS = 1, OUT_QKV = 2, OUT_SWIGLU = 3;
+// epilogue, the gated feed-forward epilogue, and the query heads attended over chunks of the
+// cached keys (with the new key and value rows) in one launch.
+constexpr int OUT_STORE = 0, OUT_DOTS = 1, OUT_QKV = 2, OUT_SWIGLU = 3, OUT_QATTN = 4;
 
 struct ProjParams {
     const int8_t *codes, *codes2;      // device table(s); codes2 is the SwiGLU up table
@@ -24,6 +26,7 @@ struct ProjParams {
     // + w % qstride: consecutive quads when qstride is 1; the two halves of a rotary pair (quads
     // D/8 apart) when the QKV epilogue asks for qstride = D/8, qpw = 2.
     int quad_begin, quad_end, qpw, qstride;
+    int qshift;  // log2 qstride (set by the launcher)
     // input
     const float *x;
     const int8_t *q;
@@ -32,7 +35,9 @@ struct ProjParams {
     int zp;
     const float *norm_w;
     float eps;
-    const float *part;  // IN_ATTN: per (head, chunk) records of D + 4 floats: max, total, -, -, sums
+    // IN_ATTN: per (head, chunk) records of D + 4 floats (max, total, -, -, sums), merged with the
+    // new key's own state (rotated query in qkv_out, key and value at the position in the caches)
+    const float *part;
     int chunks;
     // store
     const float *bias;
@@ -52,11 +57,16 @@ struct ProjParams {
     int capacity, position;
     // SwiGLU epilogue: silu(gate)·up, f32 (the down projection quantizes it in its prologue)
     float *act_out;
+    // OUT_QATTN: workgroup w < heads·chunks projects query head w / chunks (its D rows) and attends
+    // over keys [c·per_chunk, min((c + 1)·per_chunk, position)) of chunk c = w % chunks, writing the
+    // chunk's record to `states`; the rest project the key and value rows in rotary pairs
+    int per_chunk;
+    float *states;
 };
 
 // Byte offsets of the LDS regions (every region 16-byte aligned).
 struct ProjLayout {
-    int off_s, off_c, off_red, off_y, off_terms, off_n, total;
+    int off_s, off_c, off_red, off_y, off_terms, off_n, off_att, total;
 };
 
 __host__ __device__ inline int align16(int b) { return (b + 15) & ~15; }
@@ -72,7 +82,10 @@ __host__ __device__ inline ProjLayout proj_layout(int R, int K, int G, int NW, i
     l.off_y = l.off_red + 16 * 4;
     l.off_terms = l.off_y + align16(ny * R * NW * 4);
     l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * NW * ((G + 3) & ~3) * 4));
-    l.total = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);  // the exact RMSNorm's row
+    l.off_att = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);  // the exact RMSNorm's row
+    // OUT_QATTN: the rotated query [NW = D], the tile's weights [kTileKeys], maxima and totals [8],
+    // the weighted sums' partials [256]
+    l.total = l.off_att + (out == OUT_QATTN ? align16((NW + kTileKeys + 8 + 256) * 4) : 0);
     return l;
 }
 

@@ -32,7 +32,6 @@ constexpr int kScoreKeys = 32;   // keys per workgroup of the scores
 constexpr int kWeighKeys = 256;  // keys per staged chunk of values
 constexpr int kWeighDims = 32;   // value dimensions per workgroup (one quantization group)
 constexpr int kHeadQuads = 16;  // quads per workgroup of the logits product
-constexpr int kTileKeys = 64;   // keys per tile of the fast attention
 
 struct AttnParams {
     const float *qkv;  // rotated query heads first
@@ -40,8 +39,6 @@ struct AttnParams {
     size_t layer_base;
     int heads, kv_heads, D, capacity, keys;
     float *scores;  // [heads][capacity]
-    float *part;    // fast attention: [heads][chunks][D + 4]
-    int chunks, per_chunk;
     int zp;
     int8_t *q;
     float *scales;
@@ -256,89 +253,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
     }
 }
 
-// The fast (parallel-order) attention, first half: the softmax state of one query head over one
-// chunk of keys (flash decoding). Per tile of kTileKeys keys: the scores q·k_j·(1/√D) (ops.rs:310-
-// 326; four lanes per key), the running maximum m, e^(s_j − m) through ops::exp, the running total
-// l and the running weighted sum of values (ops.rs:329-342), both rescaled by e^(m_old − m) when
-// the maximum moves. Writes (m, l, −, −, acc[D]) per (head, chunk); the output projection's
-// prologue merges the chunks. Grid: (heads, chunks).
-template <int D>
-__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(AttnParams a)
-{
-    __shared__ float pw[kTileKeys];
-    __shared__ float red[8];
-    __shared__ float sums[kAttnThreads];
-    constexpr int DQ = D / 4;             // dims of a key per lane
-    constexpr int KG = kAttnThreads / D;  // key groups of the weighted sum
-    constexpr int VK = kTileKeys / KG;    // values per lane per tile
-    const int head = blockIdx.x, c = blockIdx.y;
-    const int kv = head / (a.heads / a.kv_heads);
-    const int first = c * a.per_chunk, last = min(a.keys, first + a.per_chunk);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int jk = tid >> 2, part = tid & 3;  // scores: key jk of the tile, dims part·DQ ..
-    const int d = tid % D, g = tid / D;       // weighted sum: dim d over keys g, g + KG, ..
-    const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
-    const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D;
-    v4f q[DQ / 4];
-#pragma unroll
-    for (int i = 0; i < DQ / 4; i++) q[i] = *reinterpret_cast<const v4f *>(a.qkv + size_t(head) * D + part * DQ + 4 * i);
-    const float scale = 1.0f / sqrtf(float(D));
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;
-    for (int j0 = first; j0 < last; j0 += kTileKeys) {
-        const int n = min(kTileKeys, last - j0);
-        // every load of the tile first (branch-free: keys past n re-read key j0)
-        v4f k[DQ / 4];
-        const float *krow = kbase + size_t((j0 + (jk < n ? jk : 0)) % a.capacity) * D + part * DQ;
-#pragma unroll
-        for (int i = 0; i < DQ / 4; i++) k[i] = *reinterpret_cast<const v4f *>(krow + 4 * i);
-        float v[VK];
-#pragma unroll
-        for (int e = 0; e < VK; e++) {
-            const int j = g + e * KG;
-            v[e] = vbase[size_t((j0 + (j < n ? j : 0)) % a.capacity) * D + d];
-        }
-        v4f sv = q[0] * k[0];
-#pragma unroll
-        for (int i = 1; i < DQ / 4; i++) sv = sv + q[i] * k[i];
-        float s = (sv.x + sv.y) + (sv.z + sv.w);
-        s = s + __int_as_float(xor1(__float_as_int(s)));
-        s = s + __int_as_float(xor2(__float_as_int(s)));
-        s = jk < n ? s * scale : -INFINITY;
-        const float wm = wave_max(s);
-        if (lane == 0) red[wave] = wm;
-        __syncthreads();
-        const float m_new = fmaxf(m, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
-        const float r = m == -INFINITY ? 0.0f : ref_exp(m - m_new);
-        const float pj = jk < n ? ref_exp(s - m_new) : 0.0f;
-        const float ws = wave_sum_unordered(part == 0 ? pj : 0.0f);
-        if (part == 0) pw[jk] = pj;
-        if (lane == 0) red[4 + wave] = ws;
-        __syncthreads();
-        l = l * r + ((red[4] + red[5]) + (red[6] + red[7]));
-        m = m_new;
-        acc = acc * r;
-#pragma unroll
-        for (int e = 0; e < VK; e++) {
-            const int j = g + e * KG;
-            acc = acc + (j < n ? pw[j] * v[e] : 0.0f);
-        }
-        __syncthreads();  // pw and red are the next tile's
-    }
-    sums[tid] = acc;
-    __syncthreads();
-    float *rec = a.part + size_t(head * a.chunks + c) * (D + 4);
-    if (g == 0) {
-        float o = acc;
-#pragma unroll
-        for (int gg = 1; gg < KG; gg++) o = o + sums[gg * D + d];
-        rec[4 + d] = o;
-    }
-    if (tid == 0) {
-        rec[0] = m;
-        rec[1] = l;
-    }
-}
-
 // Prediction::greedy (lm.rs:169-179) over the head's per-workgroup candidates: the first index of
 // the largest logit; NaNs never win, and a NaN first logit keeps index 0.
 __global__ __launch_bounds__(1024) void greedy_kernel(const float *__restrict__ pval, const int32_t *__restrict__ pidx, int n,
@@ -452,11 +366,48 @@ int qkv_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position
 // Whether the attention runs as flash decoding merged by the output projection (parallel order).
 bool fast_attention(const fg_qwen2 *m) { return !m->shape.exact && m->shape.heads * m->shape.head_dim <= 1024; }
 
-// 3. and 5. a projection added to the residual row: of the attention's output (o: quantized by
-// the attention, or merged from its chunks and quantized in the prologue), or of the f32
-// silu(gate)·up row, quantized in the prologue (down).
-int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st)
+// 1.-2. in parallel order, one launch: every query head's rows (RMSNorm + quantize -> product +
+// bias -> RoPE) recomputed by each of its chunk workgroups, which then attend over their chunk of
+// the cached keys [0, position); the key and value rows of the position projected, rotated and
+// kept by the remaining workgroups. The output projection merges the chunks with the new key.
+int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position, hipStream_t st)
 {
+    const fg_qwen2_shape &sh = m->shape;
+    // chunks of whole tiles over the cached keys, at most kMaxChunks per head (at least one)
+    const int keys = int(position);
+    const int per = (keys + kMaxChunks - 1) / kMaxChunks;
+    m->per_chunk = std::max(kTileKeys, (per + kTileKeys - 1) / kTileKeys * kTileKeys);
+    m->chunks = std::max(1, (keys + m->per_chunk - 1) / m->per_chunk);
+    ProjParams p = table_params(ly.qkv);
+    p.qpw = int(sh.head_dim / 4);  // a query head's quads
+    p.qstride = 1;
+    p.x = m->hidden;
+    p.norm_w = ly.norm1;
+    p.eps = sh.eps;
+    p.zp = m->zp;
+    p.bias = ly.qkv_bias;
+    p.qkv_out = m->qkv;
+    p.rope = m->rope + position * sh.head_dim;
+    p.heads = int(sh.heads);
+    p.kv_heads = int(sh.kv_heads);
+    p.D = int(sh.head_dim);
+    p.kcache = m->kcache;
+    p.vcache = m->vcache;
+    p.layer_base = li * sh.kv_heads * sh.capacity * sh.head_dim;
+    p.capacity = int(sh.capacity);
+    p.position = int(position);
+    p.chunks = m->chunks;
+    p.per_chunk = m->per_chunk;
+    p.states = m->part;
+    return launch_proj(p, sh.dtype, IN_NORM, OUT_QATTN, false, st);
+}
+
+// 3. and 5. a projection added to the residual row: of the attention's output (o: quantized by
+// the attention, or merged from its chunks and the new key and quantized in the prologue), or of
+// the f32 silu(gate)·up row, quantized in the prologue (down).
+int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st, size_t li = 0, size_t position = 0)
+{
+    const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(t);
     p.qpw = 1;
     if (in == IN_F32) {
@@ -464,8 +415,15 @@ int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st)
     } else if (in == IN_ATTN) {
         p.part = m->part;
         p.chunks = m->chunks;
-        p.heads = int(m->shape.heads);
-        p.D = int(m->shape.head_dim);
+        p.heads = int(sh.heads);
+        p.kv_heads = int(sh.kv_heads);
+        p.D = int(sh.head_dim);
+        p.qkv_out = m->qkv;
+        p.kcache = m->kcache;
+        p.vcache = m->vcache;
+        p.layer_base = li * sh.kv_heads * sh.capacity * sh.head_dim;
+        p.capacity = int(sh.capacity);
+        p.position = int(position);
     } else {
         p.q = m->xq;
         p.as = m->xs;
@@ -512,23 +470,6 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     a.q = m->xq;
     a.scales = m->xs;
     a.corr = m->xc;
-    if (fast_attention(m)) {
-        // chunks of whole tiles, at most kMaxChunks per head
-        const int per = (a.keys + kMaxChunks - 1) / kMaxChunks;
-        m->per_chunk = std::max(kTileKeys, (per + kTileKeys - 1) / kTileKeys * kTileKeys);
-        m->chunks = (a.keys + m->per_chunk - 1) / m->per_chunk;
-        a.part = m->part;
-        a.chunks = m->chunks;
-        a.per_chunk = m->per_chunk;
-        const dim3 grid(unsigned(sh.heads), unsigned(m->chunks));
-        switch (sh.head_dim) {
-        case 32: attn_partial_kernel<32><<<grid, kAttnThreads, 0, st>>>(a); break;
-        case 64: attn_partial_kernel<64><<<grid, kAttnThreads, 0, st>>>(a); break;
-        default: attn_partial_kernel<128><<<grid, kAttnThreads, 0, st>>>(a); break;
-        }
-        FG_HIP(hipGetLastError());
-        return FG_OK;
-    }
     const dim3 sgrid(unsigned(sh.kv_heads), unsigned((a.keys + kScoreKeys - 1) / kScoreKeys));
     attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
     FG_HIP(hipGetLastError());
@@ -543,9 +484,14 @@ int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
 {
     const fg_qwen2_layer &ly = m->layers[li];
     int rc;
-    if ((rc = qkv_launch(m, ly, li, position, st))) return rc;
-    if ((rc = attention_launch(m, li, position, st))) return rc;
-    if ((rc = residual_launch(m, ly.o, fast_attention(m) ? IN_ATTN : IN_PREQ, st))) return rc;
+    if (fast_attention(m)) {
+        if ((rc = qattn_launch(m, ly, li, position, st))) return rc;
+        if ((rc = residual_launch(m, ly.o, IN_ATTN, st, li, position))) return rc;
+    } else {
+        if ((rc = qkv_launch(m, ly, li, position, st))) return rc;
+        if ((rc = attention_launch(m, li, position, st))) return rc;
+        if ((rc = residual_launch(m, ly.o, IN_PREQ, st))) return rc;
+    }
     if ((rc = swiglu_launch(m, ly, st))) return rc;
     return residual_launch(m, ly.down, IN_F32, st);
 }

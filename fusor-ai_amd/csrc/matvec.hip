@@ -308,100 +308,168 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
 // ---------------------------------------------------------------- the fast attention's chunks
 //
 // One query head over one chunk of the cached keys (flash decoding), 256 threads. Per tile of
-// kTileKeys keys: the scores q·k_j·(1/√D) (ops.rs:310-326; four lanes per key), the running maximum
-// m, e^(s_j − m) through ops::exp, the running total l and the running weighted sum of values
-// (ops.rs:329-342), both rescaled by e^(m_old − m) when the maximum moves. The chunk's record is
-// (m, l, −, −, acc[D]); the output projection's prologue merges the records with the new key's.
+// kTileKeys keys, wave w takes keys 16w .. 16w + 15: the scores q·k_j·(1/√D) (ops.rs:310-326;
+// four lanes per key), the wave's running maximum m, e^(s_j − m) through ops::exp, the running
+// total l and the running weighted sum of values (ops.rs:329-342), both rescaled by e^(m_old − m)
+// when the maximum moves; every reduction within the wave (DPP and lane broadcasts). The four
+// waves' states are merged once at the end into the chunk's record (m, l, −, −, acc[D]), which the
+// output projection's prologue merges with the other chunks' and the new key's.
 
-// A tile's keys and values as one thread holds them: for the scores, key jk = t / 4, dims
-// (t % 4)·D/4 ..; for the weighted sum, dim t % D of keys t / D, t / D + 256 / D, ...
+template <int D>
+struct AttnShape {
+    static constexpr int DQ = D / 4;                 // dims of a key per lane (scores)
+    static constexpr int KPL = D >= 64 ? 16 : 8;     // keys per lane (weighted sum)
+    static constexpr int VPL = D >= 64 ? D / 64 : 1; // dims per lane (weighted sum)
+};
+
+// A tile's keys and values as one thread holds them: for the scores, key 16w + (lane / 4), dims
+// (lane % 4)·D/4 ..; for the weighted sum, dims lane·VPL .. of the wave's 16 keys (D = 32: dim
+// lane % 32 of keys 16w + (lane / 32)·8 ..).
 template <int D>
 struct KVTile {
     v4f k[D >= 16 ? D / 16 : 1];
-    float v[D >= 4 ? D / 4 : 1];
+    float v[D >= 64 ? 16 * (D / 64) : 8];
 };
+
+template <int D>
+__device__ __forceinline__ void value_slot(int lane, int wave, int &key0, int &dim0)
+{
+    if (D >= 64) {
+        key0 = 16 * wave;
+        dim0 = lane * AttnShape<D>::VPL;
+    } else {
+        key0 = 16 * wave + (lane >> 5) * 8;
+        dim0 = lane & 31;
+    }
+}
 
 // The tile of keys j0 .. j0 + n - 1 of KV head `kv` (branch-free: keys past n re-read key j0).
 template <int D>
 __device__ __forceinline__ void load_kv_tile(const ProjParams &p, int kv, int j0, int n, KVTile<D> &t)
 {
     if (D == 0) return;
-    constexpr int DQ = D / 4, KG = kThreads / (D > 0 ? D : 1), VK = kTileKeys / (KG > 0 ? KG : 1);
-    const int tid = threadIdx.x, jk = tid >> 2, part = tid & 3, d = tid % (D > 0 ? D : 1), g = tid / (D > 0 ? D : 1);
+    using S = AttnShape<D>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, jk = tid >> 2, part = tid & 3;
     const size_t row0 = p.layer_base + (size_t(kv) * p.capacity + size_t(j0)) * D;  // the tile's first key
     const float *kt = p.kcache + row0, *vt = p.vcache + row0;
-    const unsigned koff = unsigned((jk < n ? jk : 0) * D + part * DQ);
+    const unsigned koff = unsigned((jk < n ? jk : 0) * D + part * S::DQ);
 #pragma unroll
-    for (int i = 0; i < DQ / 4; i++) t.k[i] = *reinterpret_cast<const v4f *>(kt + (koff + 4u * i));
+    for (int i = 0; i < S::DQ / 4; i++) t.k[i] = *reinterpret_cast<const v4f *>(kt + (koff + 4u * i));
+    int key0, dim0;
+    value_slot<D>(lane, wave, key0, dim0);
 #pragma unroll
-    for (int e = 0; e < VK; e++) {
-        const int j = g + e * KG;
-        t.v[e] = vt[unsigned((j < n ? j : 0) * D + d)];
+    for (int e = 0; e < S::KPL; e++) {
+        const int j = key0 + e;
+        const unsigned at = unsigned((j < n ? j : 0) * D + dim0);
+        if (S::VPL == 2) {
+            const float2 v2 = *reinterpret_cast<const float2 *>(vt + at);
+            t.v[2 * e] = v2.x;
+            t.v[2 * e + 1] = v2.y;
+        } else {
+            t.v[e] = vt[at];
+        }
     }
 }
 
+// Maximum / sum over the wave of a value held by every lane (DPP within rows of 16, then lane
+// exchanges across rows).
+__device__ __forceinline__ float wave_allmax(float v)
+{
+    v = fmaxf(v, __int_as_float(xor1(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(xor2(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(mirror8(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));  // row_ror:8
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float wave_allsum(float v)
+{
+    v = v + __int_as_float(xor1(__float_as_int(v)));
+    v = v + __int_as_float(xor2(__float_as_int(v)));
+    v = v + __int_as_float(mirror8(__float_as_int(v)));
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+    v = v + __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
 // Chunk c of query head h: keys [c·per_chunk, min((c + 1)·per_chunk, position)); the first tile is
-// already in `tile`. `scratch` holds kTileKeys + 8 + 256 floats of LDS.
+// already in `tile`. `scratch` holds 8 + 4·D floats of LDS.
 template <int D>
 __device__ __forceinline__ void attend_chunk(const ProjParams &p, const float *qrot, int h, int c, KVTile<D> &tile,
                                              float *scratch)
 {
     if (D == 0) return;
-    constexpr int DQ = D / 4, KG = kThreads / (D > 0 ? D : 1), VK = kTileKeys / (KG > 0 ? KG : 1);
-    float *pw = scratch;            // [kTileKeys] the tile's weights
-    float *red = pw + kTileKeys;    // [8] per-wave maxima and totals
-    float *sums = red + 8;          // [256] the weighted sums' partials
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int jk = tid >> 2, part = tid & 3, d = tid % (D > 0 ? D : 1), g = tid / (D > 0 ? D : 1);
+    using S = AttnShape<D>;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, jk = tid >> 2, part = tid & 3;
     const int kv = h / (p.heads / p.kv_heads);
     const int first = c * p.per_chunk, last = min(p.position, first + p.per_chunk);
-    v4f q[DQ / 4 > 0 ? DQ / 4 : 1];
+    int key0, dim0;
+    value_slot<D>(lane, wave, key0, dim0);
+    v4f q[S::DQ / 4 > 0 ? S::DQ / 4 : 1];
 #pragma unroll
-    for (int i = 0; i < DQ / 4; i++) q[i] = *reinterpret_cast<const v4f *>(qrot + part * DQ + 4 * i);
+    for (int i = 0; i < S::DQ / 4; i++) q[i] = *reinterpret_cast<const v4f *>(qrot + part * S::DQ + 4 * i);
     const float scale = 1.0f / sqrtf(float(D));
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    float acc[S::VPL];
+#pragma unroll
+    for (int i = 0; i < S::VPL; i++) acc[i] = 0.0f;
     for (int j0 = first; j0 < last; j0 += kTileKeys) {
         const int n = min(kTileKeys, last - j0);
         if (j0 != first) load_kv_tile<D>(p, kv, j0, n, tile);
         v4f sv = q[0] * tile.k[0];
 #pragma unroll
-        for (int i = 1; i < DQ / 4; i++) sv = sv + q[i] * tile.k[i];
+        for (int i = 1; i < S::DQ / 4; i++) sv = sv + q[i] * tile.k[i];
         float sc = (sv.x + sv.y) + (sv.z + sv.w);
         sc = sc + __int_as_float(xor1(__float_as_int(sc)));
         sc = sc + __int_as_float(xor2(__float_as_int(sc)));
         sc = jk < n ? sc * scale : -INFINITY;
-        const float wm = wave_max(sc);
-        if (lane == 0) red[wave] = wm;
-        __syncthreads();
-        const float m_new = fmaxf(m, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        const float m_new = fmaxf(m, wave_allmax(sc));
+        if (m_new == -INFINITY) continue;  // no key of this tile in this wave (uniform)
         const float r = m == -INFINITY ? 0.0f : ref_exp(m - m_new);
         const float pj = jk < n ? ref_exp(sc - m_new) : 0.0f;
-        const float ws = wave_sum_unordered(part == 0 ? pj : 0.0f);
-        if (part == 0) pw[jk] = pj;
-        if (lane == 0) red[4 + wave] = ws;
-        __syncthreads();
-        l = l * r + ((red[4] + red[5]) + (red[6] + red[7]));
+        l = l * r + wave_allsum(part == 0 ? pj : 0.0f);
         m = m_new;
-        acc = acc * r;
 #pragma unroll
-        for (int e = 0; e < VK; e++) {
-            const int j = g + e * KG;
-            acc = acc + (j < n ? pw[j] * tile.v[e] : 0.0f);
+        for (int i = 0; i < S::VPL; i++) acc[i] = acc[i] * r;
+#pragma unroll
+        for (int e = 0; e < S::KPL; e++) {
+            // key key0 + e's weight, from lane 4·(key0 + e − 16·wave) of this wave
+            float w;
+            if (D >= 64) w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), 4 * e));
+            else w = __shfl(pj, 4 * (key0 + e - 16 * wave), 64);
+#pragma unroll
+            for (int i = 0; i < S::VPL; i++) acc[i] = acc[i] + w * tile.v[S::VPL * e + i];
         }
-        __syncthreads();  // pw and red are the next tile's
     }
-    sums[tid] = acc;
+    if (D < 64) acc[0] = acc[0] + __shfl_xor(acc[0], 32, 64);  // the two halves' keys, same dims
+    // the waves' states merged: M = max m_w, L = Σ l_w·e^(m_w − M), acc = Σ acc_w·e^(m_w − M)
+    float *wm = scratch, *wl = scratch + 4, *wacc = scratch + 8;  // [4], [4], [4][D]
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
+    if (D >= 64 || lane < 32) {
+#pragma unroll
+        for (int i = 0; i < S::VPL; i++) wacc[wave * D + dim0 + i] = acc[i];
+    }
     __syncthreads();
     float *rec = p.states + size_t(h * p.chunks + c) * (D + 4);
-    if (g == 0) {
-        float o = acc;
+    if (tid < D) {
+        const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+        float L = 0.0f, o = 0.0f;
+        if (M != -INFINITY) {
 #pragma unroll
-        for (int gg = 1; gg < KG; gg++) o = o + sums[gg * D + d];
-        rec[4 + d] = o;
-    }
-    if (tid == 0) {
-        rec[0] = m;
-        rec[1] = l;
+            for (int w = 0; w < 4; w++) {
+                const float e = wm[w] == -INFINITY ? 0.0f : ref_exp(wm[w] - M);
+                L = L + wl[w] * e;
+                o = o + wacc[w * D + tid] * e;
+            }
+        }
+        rec[4 + tid] = o;
+        if (tid == 0) {
+            rec[0] = M;
+            rec[1] = L;
+        }
     }
 }
 
@@ -638,8 +706,8 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
 
     // Output i of (table, row, column): bias, then stored (written or added to the residual row).
     auto finish = [&](int i, float s) {
-        const int tb = i / (R * NW), rem = i - tb * R * NW;
-        const int r = rem / NW, nl = rem - r * NW;
+        const int tb = NT == 1 ? 0 : i / (R * NW), rem = i - tb * R * NW;  // no division where fixed
+        const int r = R == 1 ? 0 : rem / NW, nl = rem - r * NW;
         const int n = output_of(nl);
         if (OUT != OUT_SWIGLU && p.bias && n < p.n_rows) s = s + (i == my_out ? bias0 : p.bias[n]);
         if (OUT == OUT_STORE) {
@@ -650,13 +718,18 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         }
         ybuf[i] = s;
     };
-    auto live = [&](int i) { return i < outs && (i % NW) < nq * 4; };
+    auto live = [&](int i) { return i < outs && (NT * R == 1 ? i : i % NW) < nq * 4; };
     if (TREE) {
         // strided partial sums, then the team's lanes reduced (lanes of one wave)
         float s = 0.0f;
         if (live(my_out)) {
-            const float *t = terms + my_out * Gp;  // [tb][r][nl] rows in output order
-            for (int g = sub; g < G; g += team) s = s + t[g];
+            // [tb][r][nl] rows in output order, 16-byte aligned: four terms per read
+            const v4f *t4 = reinterpret_cast<const v4f *>(terms + my_out * Gp);
+            for (int k = sub; 4 * k < G; k += team) {
+                const v4f v = t4[k];
+                const int g = 4 * k;
+                s = s + ((v.x + (g + 1 < G ? v.y : 0.0f)) + ((g + 2 < G ? v.z : 0.0f) + (g + 3 < G ? v.w : 0.0f)));
+            }
         }
         if (team >= 2) s = s + __int_as_float(xor1(__float_as_int(s)));
         if (team >= 4) s = s + __int_as_float(xor2(__float_as_int(s)));

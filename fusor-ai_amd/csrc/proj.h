@@ -83,9 +83,8 @@ __host__ __device__ inline ProjLayout proj_layout(int R, int K, int G, int NW, i
     l.off_terms = l.off_y + align16(ny * R * NW * 4);
     l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * NW * ((G + 3) & ~3) * 4));
     l.off_att = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);  // the exact RMSNorm's row
-    // OUT_QATTN: the rotated query [NW = D], the tile's weights [kTileKeys], maxima and totals [8],
-    // the weighted sums' partials [256]
-    l.total = l.off_att + (out == OUT_QATTN ? align16((NW + kTileKeys + 8 + 256) * 4) : 0);
+    // OUT_QATTN: the rotated query [NW = D], the waves' maxima and totals [8] and weighted sums [4][D]
+    l.total = l.off_att + (out == OUT_QATTN ? align16((NW + 8 + 4 * NW) * 4) : 0);
     return l;
 }
 

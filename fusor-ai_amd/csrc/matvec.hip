@@ -133,8 +133,8 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
     } else if (IN == IN_ATTN) {
         // lane t merges float4 t of the attention row (head t·4 / D); every chunk's record at once
         const int e = min(tid, K / 4 - 1);
-        const int h = e * 4 / p.D, d4 = e * 4 - h * p.D;
-        const size_t at = p.layer_base + (size_t(h / (p.heads / p.kv_heads)) * p.capacity + size_t(p.position)) * p.D + d4;
+        const int h = (e * 4) >> p.dshift, d4 = e * 4 - h * p.D;
+        const size_t at = p.layer_base + (size_t(divq(h, p.rcp_group)) * p.capacity + size_t(p.position)) * p.D + d4;
         g.qn = *reinterpret_cast<const v4f *>(p.qkv_out + size_t(h) * p.D + d4);
         g.kn = *reinterpret_cast<const v4f *>(p.kcache + at);
         g.vn = *reinterpret_cast<const v4f *>(p.vcache + at);
@@ -401,7 +401,7 @@ __device__ __forceinline__ void attend_chunk(const ProjParams &p, const float *q
     if (D == 0) return;
     using S = AttnShape<D>;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, jk = tid >> 2, part = tid & 3;
-    const int kv = h / (p.heads / p.kv_heads);
+    const int kv = divq(h, p.rcp_group);
     const int first = c * p.per_chunk, last = min(p.position, first + p.per_chunk);
     int key0, dim0;
     value_slot<D>(lane, wave, key0, dim0);
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         constexpr int hq = HD / 8;
         const int b = w - qwgs;
         qs = query ? 1 : hq;
-        base = query ? qattn_unit(p, w, qwgs) / p.chunks * (HD / 4) : p.heads * (HD / 4) + b / hq * hq * 2 + b % hq;
+        base = query ? divq(qattn_unit(p, w, qwgs), p.rcp_chunks) * (HD / 4) : p.heads * (HD / 4) + b / hq * hq * 2 + b % hq;
         nq = query ? HD / 4 : 2;
     } else {
         qs = p.qstride;
@@ -555,7 +555,8 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             cu.ql++;
         }
     };
-    Cursor ccur{qb0 / B, qb0 % B};
+    const int ql0 = divq(qb0, p.rcp_B);
+    Cursor ccur{ql0, qb0 - ql0 * B};
 
     // The workgroup's quad blocks, numbered ql·B + blk, sit contiguously from its first quad, but
     // for a strided pair (qs > 1, two quads) whose second half starts (qs − 1)·B blocks later.
@@ -678,10 +679,10 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     int head = 0, chunk = 0;
     if (OUT == OUT_QATTN) {
         const int unit = query ? qattn_unit(p, int(blockIdx.x), qwgs) : 0;
-        head = unit / p.chunks;
-        chunk = unit % p.chunks;
+        head = divq(unit, p.rcp_chunks);
+        chunk = unit - head * p.chunks;
         const int first = chunk * p.per_chunk;
-        load_kv_tile<HD>(p, head / (p.heads / p.kv_heads), first, max(0, min(kTileKeys, min(p.position, first + p.per_chunk) - first)), tile);
+        load_kv_tile<HD>(p, divq(head, p.rcp_group), first, max(0, min(kTileKeys, min(p.position, first + p.per_chunk) - first)), tile);
         __builtin_amdgcn_sched_barrier(0);
     }
     stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
@@ -949,6 +950,7 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     if (p.qstride < 1) p.qstride = 1;
     if (p.qstride & (p.qstride - 1)) return set_error(FG_ERR_SHAPE, "the quad stride is a power of two");
     p.qshift = __builtin_ctz(unsigned(p.qstride));
+    proj_derive(p);
     const int span = p.qstride * p.qpw;
     if (p.qstride > 1 && (nq % span || p.qpw != 2)) return set_error(FG_ERR_SHAPE, "strided quads come in whole pairs");
     if (out == OUT_QKV && (p.qpw != 2 || p.qstride * 8 != p.D))
@@ -1032,6 +1034,7 @@ int launch_matvec(const ProductArgs &a, hipStream_t s)
     qpw = std::min(16, std::max(qpw, (nq + 2399) / 2400));
     p.qpw = qpw;
     p.qstride = 1;
+    proj_derive(p);
     while (qpw > 1 && proj_smem(p, rows, in, out) > 64 * 1024) p.qpw = qpw = qpw / 2;
     const size_t smem = proj_smem(p, rows, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");

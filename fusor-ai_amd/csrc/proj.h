@@ -27,6 +27,9 @@ struct ProjParams {
     // D/8 apart) when the QKV epilogue asks for qstride = D/8, qpw = 2.
     int quad_begin, quad_end, qpw, qstride;
     int qshift;  // log2 qstride (set by the launcher)
+    // Set by the launcher (proj_derive): reciprocals for exact small quotients (divq), log2 D
+    float rcp_B, rcp_chunks, rcp_group;
+    int dshift;
     // input
     const float *x;
     const int8_t *q;
@@ -63,6 +66,19 @@ struct ProjParams {
     int per_chunk;
     float *states;
 };
+
+// a / b for 0 <= a < 2^22 and b >= 1 from rcp = fl(1/b): (a + 1/2)/b is at least 1/(2b) from
+// an integer, and the two roundings move it by less than that, so the floor is the quotient.
+__device__ __forceinline__ int divq(int a, float rcp) { return int((float(a) + 0.5f) * rcp); }
+
+// The launcher's derived fields of a parameter block.
+inline void proj_derive(ProjParams &p)
+{
+    p.rcp_B = 1.0f / float(p.B > 0 ? p.B : 1);
+    p.rcp_chunks = 1.0f / float(p.chunks > 0 ? p.chunks : 1);
+    p.rcp_group = 1.0f / float(p.kv_heads > 0 && p.heads >= p.kv_heads ? p.heads / p.kv_heads : 1);
+    p.dshift = p.D > 0 ? __builtin_ctz(unsigned(p.D)) : 0;
+}
 
 // Byte offsets of the LDS regions (every region 16-byte aligned).
 struct ProjLayout {

@@ -10,7 +10,9 @@
 // Mapping. A workgroup owns `qpw` quads (4 output rows each; consecutive, or a rotary pair D/8
 // quads apart) and all of their blocks (in two tables for the gated feed-forward's gate and up).
 // Its four waves stream them in 1 KiB chunks (64 lanes x 16 B, coalesced 128-bit loads),
-// `kBatch` chunks per wave in flight, the next batch issued before the current one is consumed.
+// `kBatch` chunks per wave in flight (the fewest that cover a wave's share), the next batch
+// issued before the current one is consumed. The entry is branch-free, so the parameters arrive
+// in one scalar round trip ahead of the first vector load.
 // Small workgroups (a few quads, about 16 KiB of codes) spread a small table over every CU: a
 // CU keeps a bounded number of reads in flight, so a large share per CU costs round trips.
 // The first batch is issued before the activations are staged, so the prologue (a copy, an
@@ -23,7 +25,10 @@
 // Epilogues: store (with bias, or added to a residual row, optionally each workgroup's greedy
 // candidate); QKV (bias, rotary embedding by halves of the query and key heads, the key and value
 // heads kept in the cache: rope_half ops.rs:77-85, KvCache::keep transformer.rs:166-180); SwiGLU
-// (silu(gate)·up as f32, layer.rs:321-341, which the down projection quantizes as its input).
+// (silu(gate)·up as f32, layer.rs:321-341, which the down projection quantizes as its input);
+// query attention (one query head's rows rotated, then attended over one chunk of the cached keys,
+// ops.rs:301-342 and transformer.rs:185-219 in parallel order; the key and value rows of the position
+// kept by the remaining workgroups).
 #include <algorithm>
 
 #include "common.h"

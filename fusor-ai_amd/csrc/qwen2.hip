@@ -2,7 +2,8 @@
 // Prediction::predict (blocks/src/transformer.rs:185-341, layer.rs:161-344,
 // layer/input.rs:22-66, lm.rs:97-179), every projection through the projection kernel.
 //
-// Six launches per layer, each projection with its neighbours fused in:
+// Per layer, each projection with its neighbours fused in. In the reference's order (exact), six
+// launches:
 //   1. RMSNorm + quantize -> QKV product + bias -> RoPE on query/key heads, keys and values kept
 //   2. attention of every query head over the cache in two launches: the scores by key blocks,
 //      then softmax and weighted values by head and 32 value dimensions, quantized for the output
@@ -10,6 +11,10 @@
 //   3. output projection added to the residual row
 //   4. RMSNorm + quantize -> gate and up products -> silu(gate)·up quantized for down
 //   5. down projection added to the residual row
+// In parallel order, four: 1 and 2 become one launch whose workgroups each project one query head
+// and attend over one chunk of the cached keys (flash decoding), next to workgroups projecting the
+// position's key and value rows; the output projection's prologue merges the chunks with the new
+// key's own state.
 // then RMSNorm + quantize -> head product (logits) with per-workgroup greedy candidates, and the
 // greedy token. Elementwise arithmetic is the reference's operation for operation (no fused
 // multiply-add; ops::exp's polynomial). Reductions whose order changes f32 bits (RMSNorm's sum of

@@ -306,9 +306,13 @@ def extras(fk, torch, np):
         qr = fk.QuantizedRows()
         inp = qr.input(m, x.view(-1))
         ms_q = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 10, graph=True)
+        # the NEON backend's arithmetic (one fused multiply-add per group scaling), its own bits
+        ms_fused = timer(lambda: fk.matmul(m, inp, range(0, n), out=out, fused=True), 10, graph=True)
         ops = 2.0 * rows * n * k
         res[label] = {"with_quantization_launched_us": round(ms_f32 * 1e3, 2), "prequantized_us": round(ms_q * 1e3, 2),
-                      "TOPS": round(ops / ms_q / 1e9, 1), "frac_int8_peak": round(ops / ms_q / 1e9 / INT8_PEAK_TOPS, 4)}
+                      "TOPS": round(ops / ms_q / 1e9, 1), "frac_int8_peak": round(ops / ms_q / 1e9 / INT8_PEAK_TOPS, 4),
+                      "fused_scale_us": round(ms_fused * 1e3, 2), "fused_scale_TOPS": round(ops / ms_fused / 1e9, 1),
+                      "fused_scale_frac_int8_peak": round(ops / ms_fused / 1e9 / INT8_PEAK_TOPS, 4)}
     # 3. packed int4 14336 x 4096, rows 1 and 16
     n, k = 14336, 4096
     t = fk.Table(fk.Tensor(Q4B32, [n, k], synthetic_table(np, Q4B32, n, k, rng)))

@@ -237,6 +237,7 @@ int fg_matmul(const fg_table *t, const fg_input *in, size_t rows, size_t col_beg
     a.out = out;
     a.ld_out = ld_out;
     a.accumulate = (flags & FG_ACCUMULATE) != 0;
+    a.fused = (flags & FG_FUSED_SCALE) != 0;
     return launch_product(a, as_stream(stream));
 }
 

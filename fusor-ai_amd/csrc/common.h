@@ -318,6 +318,7 @@ struct ProductArgs {
     size_t ld_out;
     int accumulate;
     int32_t *dots;  // when set, the int32 group accumulators are written instead of out
+    int fused;      // FG_FUSED_SCALE: s = fma((float)D, ws·as, s)
 };
 int launch_matvec(const ProductArgs &a, hipStream_t s);
 int launch_gemm(const ProductArgs &a, hipStream_t s);

@@ -57,7 +57,7 @@ struct Stage {
 
 // LDS_SCALES: the tile's activation scales for every block staged in LDS once (32 floats per
 // block), so that the ring of registers holds operands only (more waves per SIMD).
-template <int FMT, int TN, bool DOTS, bool LDS_SCALES>
+template <int FMT, int TN, bool DOTS, bool LDS_SCALES, bool FUSED>
 __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
 {
     extern __shared__ __align__(16) float tile_scales[];  // [B][32] when LDS_SCALES
@@ -141,7 +141,9 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
                 continue;
             }
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[t][v] = acc[t][v] + float(d[v]) * (st.ws[t] * sc[v]);
+            for (int v = 0; v < 16; v++)
+                acc[t][v] = FUSED ? __builtin_fmaf(float(d[v]), st.ws[t] * sc[v], acc[t][v])
+                                  : acc[t][v] + float(d[v]) * (st.ws[t] * sc[v]);
         }
     };
 
@@ -196,7 +198,7 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
 // 8·(l/16) .. +7 of the block; result: lane l holds column l % 16, rows 4·(l/16) + v, v = 0..3.
 constexpr int kDepthW = 8, kDepthA = 8;
 
-template <int FMT, bool DOTS>
+template <int FMT, bool DOTS, bool FUSED>
 __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
 {
     extern __shared__ __align__(16) float tile_scales[];  // [B][16]
@@ -256,10 +258,17 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
                 } else {
                     const float ws = rs[k];
                     const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + bb * 16 + 4 * s);
-                    acc[0] = acc[0] + float(d[0]) * (ws * sc.x);
-                    acc[1] = acc[1] + float(d[1]) * (ws * sc.y);
-                    acc[2] = acc[2] + float(d[2]) * (ws * sc.z);
-                    acc[3] = acc[3] + float(d[3]) * (ws * sc.w);
+                    if (FUSED) {
+                        acc[0] = __builtin_fmaf(float(d[0]), ws * sc.x, acc[0]);
+                        acc[1] = __builtin_fmaf(float(d[1]), ws * sc.y, acc[1]);
+                        acc[2] = __builtin_fmaf(float(d[2]), ws * sc.z, acc[2]);
+                        acc[3] = __builtin_fmaf(float(d[3]), ws * sc.w, acc[3]);
+                    } else {
+                        acc[0] = acc[0] + float(d[0]) * (ws * sc.x);
+                        acc[1] = acc[1] + float(d[1]) * (ws * sc.y);
+                        acc[2] = acc[2] + float(d[2]) * (ws * sc.z);
+                        acc[3] = acc[3] + float(d[3]) * (ws * sc.w);
+                    }
                 }
             }
             const int nw = min(bb + kDepthW, B - 1), na = min(bb + kDepthA, B - 1);
@@ -291,14 +300,14 @@ __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int
 }
 
 // 32 x 64 tiles per wave where they still give every SIMD a wave or more, else 32 x 32.
-template <int FMT>
-int launch_tiles(const GemmParams &p, bool dots, bool lds, hipStream_t s)
+template <int FMT, bool FUSED>
+int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
 {
     const int ncols = p.col_end - p.col_begin;
     if (p.M <= 16 && (dots || lds)) {
         const dim3 grid(unsigned((ncols + 15) / 16));
-        if (dots) gemm16_kernel<FMT, true><<<grid, 64, 0, s>>>(p);
-        else gemm16_kernel<FMT, false><<<grid, 64, size_t(p.B) * 16 * 4, s>>>(p);
+        if (dots) gemm16_kernel<FMT, true, false><<<grid, 64, 0, s>>>(p);
+        else gemm16_kernel<FMT, false, FUSED><<<grid, 64, size_t(p.B) * 16 * 4, s>>>(p);
         FG_HIP(hipGetLastError());
         return FG_OK;
     }
@@ -306,17 +315,24 @@ int launch_tiles(const GemmParams &p, bool dots, bool lds, hipStream_t s)
     const size_t smem = size_t(p.B) * 32 * 4;
     if (wide_waves >= 1024) {
         dim3 grid(unsigned((ncols + 63) / 64), unsigned((p.M + 31) / 32));
-        if (dots) gemm_kernel<FMT, 2, true, false><<<grid, 64, 0, s>>>(p);
-        else if (lds) gemm_kernel<FMT, 2, false, true><<<grid, 64, smem, s>>>(p);
-        else gemm_kernel<FMT, 2, false, false><<<grid, 64, 0, s>>>(p);
+        if (dots) gemm_kernel<FMT, 2, true, false, false><<<grid, 64, 0, s>>>(p);
+        else if (lds) gemm_kernel<FMT, 2, false, true, FUSED><<<grid, 64, smem, s>>>(p);
+        else gemm_kernel<FMT, 2, false, false, FUSED><<<grid, 64, 0, s>>>(p);
     } else {
         dim3 grid(unsigned((ncols + 31) / 32), unsigned((p.M + 31) / 32));
-        if (dots) gemm_kernel<FMT, 1, true, false><<<grid, 64, 0, s>>>(p);
-        else if (lds) gemm_kernel<FMT, 1, false, true><<<grid, 64, smem, s>>>(p);
-        else gemm_kernel<FMT, 1, false, false><<<grid, 64, 0, s>>>(p);
+        if (dots) gemm_kernel<FMT, 1, true, false, false><<<grid, 64, 0, s>>>(p);
+        else if (lds) gemm_kernel<FMT, 1, false, true, FUSED><<<grid, 64, smem, s>>>(p);
+        else gemm_kernel<FMT, 1, false, false, FUSED><<<grid, 64, 0, s>>>(p);
     }
     FG_HIP(hipGetLastError());
     return FG_OK;
+}
+
+// 32 x 64 tiles per wave where they still give every SIMD a wave or more, else 32 x 32.
+template <int FMT>
+int launch_tiles(const GemmParams &p, bool dots, bool lds, bool fused, hipStream_t s)
+{
+    return fused && !dots ? launch_tiles_as<FMT, true>(p, dots, lds, s) : launch_tiles_as<FMT, false>(p, dots, lds, s);
 }
 
 // T2b128 (ternary levels, one scale per 128 inputs: matmul.rs:461-469, quant.rs:168-177): one
@@ -327,7 +343,7 @@ __global__ __launch_bounds__(256) void t2_product_kernel(const uint8_t *__restri
                                                          int B, int G, int K, int n_rows, const int8_t *__restrict__ q,
                                                          const float *__restrict__ as, const int32_t *__restrict__ corr,
                                                          int rows, int col_begin, int ncols, const float *__restrict__ bias,
-                                                         float *out, long ld_out, int accumulate, int32_t *dots)
+                                                         float *out, long ld_out, int accumulate, int32_t *dots, int fused)
 {
     const long id = long(blockIdx.x) * blockDim.x + threadIdx.x;
     if (id >= long(rows) * ncols) return;
@@ -350,7 +366,8 @@ __global__ __launch_bounds__(256) void t2_product_kernel(const uint8_t *__restri
             dots[(size_t(r) * ncols + c) * G + g] = D;
             continue;
         }
-        s = s + float(D) * (wscales[(size_t(quad) * G + g) * 4 + L] * as[size_t(r) * G + g]);
+        const float sc = wscales[(size_t(quad) * G + g) * 4 + L] * as[size_t(r) * G + g];
+        s = fused ? __builtin_fmaf(float(D), sc, s) : s + float(D) * sc;
     }
     if (dots) return;
     if (bias && n < n_rows) s = s + bias[n];
@@ -384,7 +401,7 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         const long n = long(M) * ncols;
         t2_product_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint8_t *>(t->codes), t->scales, int(t->blocks),
                                                                    G, K, int(t->rows), q, as, corr, M, col_begin, ncols, a.bias,
-                                                                   a.out, long(a.ld_out), a.accumulate, a.dots);
+                                                                   a.out, long(a.ld_out), a.accumulate, a.dots, a.fused);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) rc = check_hip(e, "t2_product_kernel");
     }
@@ -451,7 +468,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.accumulate = a.accumulate;
         p.dots = a.dots;
         p.dots_cols = p.col_end - p.col_begin;
-        rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, lds, s) : launch_tiles<8>(p, dots, lds, s);
+        rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, lds, a.fused != 0, s) : launch_tiles<8>(p, dots, lds, a.fused != 0, s);
     }
     if (ws) {
         hipError_t e = hipFreeAsync(ws, s);
@@ -460,13 +477,14 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
     return rc;
 }
 
-// Rows 1..4 stream the weights once through the matrix-vector kernel; more rows go to the
-// matrix cores.
+// Rows 1..4 stream the weights once through the matrix-vector kernel; more rows (and the fused
+// scaling) go to the matrix cores.
 int launch_product(const ProductArgs &a, hipStream_t s)
 {
     if (a.rows == 0 || a.quad_end <= a.quad_begin) return FG_OK;
     if (a.t->dtype == FG_T2B128) return launch_t2(a, s);
-    if (a.rows <= 4) return launch_matvec(a, s);
+    // the matrix-vector kernel sums separately rounded terms; the fused scaling runs on the tiles
+    if (a.rows <= 4 && !a.fused) return launch_matvec(a, s);
     return launch_gemm(a, s);
 }
 

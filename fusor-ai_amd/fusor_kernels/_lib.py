@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(HERE, "libfusor_gpu.so")
 
 FG_OK, FG_ERR_SHAPE, FG_ERR_FORMAT, FG_ERR_HIP, FG_ERR_NOMEM, FG_ERR_ARG = range(6)
 FG_ACCUMULATE = 1
+FG_FUSED_SCALE = 2
 
 _P = ctypes.c_void_p
 _S = ctypes.c_size_t

@@ -134,11 +134,13 @@ def _check_input(weights, x):
         raise ShapeError("the input is prepared for the weights' format")  # matmul.rs:301-304
 
 
-def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False):
+def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False, fused=False):
     """matmul (matmul.rs:265-276) over output columns `cols` (a range of whole quads).
 
     Returns the device tensor [rows, len(cols)] of results; with `store`, also calls
-    store(row, first_col, [4 floats]) per row and quad, in the reference's order.
+    store(row, first_col, [4 floats]) per row and quad, in the reference's order. The results are
+    the scalar backend's bits, or with `fused` the NEON backend's (each group's total scaled with
+    one fused multiply-add, arch/neon.rs:140-154).
     """
     import torch
     if cols.start % QUAD or cols.stop % QUAD:
@@ -150,7 +152,8 @@ def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False):
         out = torch.empty((rows, width), dtype=torch.float32, device="cuda")
     inp = x.ffi()
     check(lib().fg_matmul(weights.table.handle, ctypes.byref(inp), rows, cols.start, cols.stop, ptr(bias), ptr(out),
-                          out.stride(0) if out.dim() == 2 else width, _lib.FG_ACCUMULATE if accumulate else 0,
+                          out.stride(0) if out.dim() == 2 else width,
+                          (_lib.FG_ACCUMULATE if accumulate else 0) | (_lib.FG_FUSED_SCALE if fused else 0),
                           stream_handle()))
     if store is not None:
         host = out.cpu().numpy()

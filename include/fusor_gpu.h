@@ -42,6 +42,11 @@ extern "C" {
 
 /* Flags of fg_matmul. */
 #define FG_ACCUMULATE 1 /* out += result: project_residual_input (linear.rs:134-143) */
+/* Scale each group's total with one fused multiply-add, s = fma((float)D, fl(ws * as), s), the
+ * reference's NEON backend (arch/neon.rs:140-154, vfmaq_f32), instead of the scalar backend's
+ * separately rounded s + (float)D * (ws * as) (arch/scalar.rs:80-89). Groups stay in order, so the
+ * f32 results are the NEON backend's bits. Rows 1..4 then take the matrix cores too. */
+#define FG_FUSED_SCALE 2
 
 /* The last failure's message on this thread ("" when none). */
 const char *fg_last_error(void);
@@ -120,7 +125,8 @@ typedef struct {
 /* matmul + Linear::project_quads (matmul.rs:265-317, linear.rs:52-71): for every input row r
  * and output column c in [col_begin, col_end) (whole quads, within the table's padded rows),
  * out[r * ld_out + (c - col_begin)] = row r · W[c] (+ bias[c] when `bias` is set), written, or
- * added with FG_ACCUMULATE. f32 results are bit-identical to the reference's scalar backend. */
+ * added with FG_ACCUMULATE. f32 results are bit-identical to the reference's scalar backend, or
+ * with FG_FUSED_SCALE to its NEON backend. */
 int fg_matmul(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
               size_t col_end, const float *bias, float *out, size_t ld_out, int flags, void *stream);
 

@@ -264,6 +264,7 @@ typedef struct {
     const int8_t *x;
     const float *x_scales;
     const int32_t *x_corrections;
+    int fused; /* the NEON backend's Backend::scale: one fused multiply-add (arch/neon.rs:140-154) */
 } product;
 
 /* Format::chunk (matmul.rs:443-469): code `i` of a word's chunk `part`. */
@@ -322,8 +323,12 @@ static void quad_pass(const product *p, size_t first_row, int rows, size_t first
                 const float *cs = p->scales + ((first_quad + (size_t)q) * p->groups + group) * OR_QUAD;
                 for (int l = 0; l < OR_QUAD; l++) { /* Backend::scale (scalar.rs:81-90) */
                     float product = cs[l] * row_scale;
-                    float term = (float)dots[r][q][l] * product;
-                    sums[r][q][l] = sums[r][q][l] + term;
+                    if (p->fused) { /* vfmaq_f32(sums, vcvtq_f32_s32(dots), column_scales * row_scale) */
+                        sums[r][q][l] = fmaf((float)dots[r][q][l], product, sums[r][q][l]);
+                    } else {
+                        float term = (float)dots[r][q][l] * product;
+                        sums[r][q][l] = sums[r][q][l] + term;
+                    }
                 }
                 if (dots_out) {
                     for (int l = 0; l < OR_QUAD; l++) {
@@ -348,6 +353,14 @@ int or_matmul(int dtype, size_t n_rows, size_t cols, const uint8_t *bytes, const
               const float *scales, const int32_t *corrections, size_t rows, size_t col_begin,
               size_t col_end, const float *bias, float *out, size_t ld_out, int32_t *dots)
 {
+    return or_matmul_fused(dtype, n_rows, cols, bytes, quants, scales, corrections, rows, col_begin, col_end, bias,
+                           out, ld_out, dots, 0);
+}
+
+int or_matmul_fused(int dtype, size_t n_rows, size_t cols, const uint8_t *bytes, const int8_t *quants,
+                    const float *scales, const int32_t *corrections, size_t rows, size_t col_begin,
+                    size_t col_end, const float *bias, float *out, size_t ld_out, int32_t *dots, int fused)
+{
     if (dtype == OR_F32 || cols % (size_t)or_group(dtype) != 0) return -1;
     if (col_begin % OR_QUAD || col_end % OR_QUAD || col_end < col_begin) return -1;
     size_t padded_rows = (n_rows + OR_QUAD - 1) / OR_QUAD * OR_QUAD;
@@ -365,6 +378,7 @@ int or_matmul(int dtype, size_t n_rows, size_t cols, const uint8_t *bytes, const
     p.x = quants;
     p.x_scales = scales;
     p.x_corrections = corrections;
+    p.fused = fused;
     size_t first = col_begin / OR_QUAD, end = col_end / OR_QUAD;
     size_t out_cols = col_end - col_begin;
     /* quant_matmul: ROWS_PER_CALL rows per call of quant_tiles, TILE rows per tile (matmul.rs:409-577) */

@@ -95,6 +95,13 @@ int or_matmul(int dtype, size_t n_rows, size_t cols, const uint8_t *bytes, const
               const float *scales, const int32_t *corrections, size_t rows, size_t col_begin,
               size_t col_end, const float *bias, float *out, size_t ld_out, int32_t *dots);
 
+/* or_matmul with the reference's NEON backend arithmetic when `fused` is set: each group's total
+ * scaled with one fused multiply-add, s = fmaf((float)D, cs * row_scale, s) (arch/neon.rs:140-154),
+ * in the same group order. */
+int or_matmul_fused(int dtype, size_t n_rows, size_t cols, const uint8_t *bytes, const int8_t *quants,
+                    const float *scales, const int32_t *corrections, size_t rows, size_t col_begin,
+                    size_t col_end, const float *bias, float *out, size_t ld_out, int32_t *dots, int fused);
+
 /* or_matmul over `threads` threads: columns split by 16 (linear.rs:113-119), or by rows when
  * rows >= outputs (conv.rs:584-589). Used for the CPU baseline only. */
 int or_matmul_threaded(int dtype, size_t n_rows, size_t cols, const uint8_t *bytes,

@@ -66,6 +66,7 @@ def _declare(l):
         "or_dequantize_row": (None, [_I, _S, _S, _P, _S, _P]),
         "or_quantize_rows": (None, [_P, _S, _I, _P, _P, _P]),
         "or_matmul": (_I, [_I, _S, _S, _P, _P, _P, _P, _S, _S, _S, _P, _P, _S, _P]),
+        "or_matmul_fused": (_I, [_I, _S, _S, _P, _P, _P, _P, _S, _S, _S, _P, _P, _S, _P, _I]),
         "or_matmul_threaded": (_I, [_I, _S, _S, _P, _P, _P, _P, _S, _P, _P, _I]),
         "or_exp": (_F, [_F]), "or_silu": (_F, [_F]),
         "or_dot_f32": (_F, [_P, _P, _S]),
@@ -160,8 +161,9 @@ def quantize_rows(x, dtype):
 
 
 def matmul(dtype, n_rows, cols, table, q, s, c, rows, col_begin=0, col_end=None, bias=None,
-           want_dots=False):
-    """The reference product of `rows` quantized rows over columns [col_begin, col_end)."""
+           want_dots=False, fused=False):
+    """The reference product of `rows` quantized rows over columns [col_begin, col_end); with
+    `fused`, the NEON backend's scaling (one fused multiply-add per group)."""
     if col_end is None:
         col_end = (n_rows + 3) // 4 * 4
     width = col_end - col_begin
@@ -176,8 +178,8 @@ def matmul(dtype, n_rows, cols, table, q, s, c, rows, col_begin=0, col_end=None,
         bias = np.ascontiguousarray(bias, dtype=np.float32)
         if bias.size < col_end:
             bias = np.concatenate([bias, np.zeros(col_end - bias.size, np.float32)])
-    rc = lib().or_matmul(dtype, n_rows, cols, _ptr(table), _ptr(q), _ptr(s), _ptr(c), rows,
-                         col_begin, col_end, _ptr(bias), _ptr(out), width, _ptr(dots))
+    rc = lib().or_matmul_fused(dtype, n_rows, cols, _ptr(table), _ptr(q), _ptr(s), _ptr(c), rows,
+                               col_begin, col_end, _ptr(bias), _ptr(out), width, _ptr(dots), int(bool(fused)))
     if rc != 0:
         raise ValueError("shape error")
     return (out, dots) if want_dots else out

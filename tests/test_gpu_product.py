@@ -161,7 +161,7 @@ def test_quantize_rows_rounds_quotients_at_every_scale(fk, dtype):
 
 # ------------------------------------------------------------------------------ products
 
-def gpu_product(fk, t, x, rows, cols=None, fused=True, bias=None, dots=False):
+def gpu_product(fk, t, x, rows, cols=None, fused=True, bias=None, dots=False, fused_scale=False):
     import torch
     m = t.matrix()
     if cols is None:
@@ -172,13 +172,15 @@ def gpu_product(fk, t, x, rows, cols=None, fused=True, bias=None, dots=False):
         inp = fk.QuantizedRows().input(m, dev(x.reshape(-1)))
     if dots:
         return host(fk.matmul_dots(m, inp, cols))
-    out = fk.matmul(m, inp, cols, bias=None if bias is None else dev(bias))
+    out = fk.matmul(m, inp, cols, bias=None if bias is None else dev(bias), fused=fused_scale)
     return host(out)
 
 
-def oracle_product(dtype, rows_w, cols_w, data, x, rows, col_begin=0, col_end=None, bias=None, want_dots=False):
+def oracle_product(dtype, rows_w, cols_w, data, x, rows, col_begin=0, col_end=None, bias=None, want_dots=False,
+                   fused=False):
     q, s, c = O.quantize_rows(x.reshape(-1), dtype)
-    return O.matmul(dtype, rows_w, cols_w, data, q, s, c, rows, col_begin, col_end, bias=bias, want_dots=want_dots)
+    return O.matmul(dtype, rows_w, cols_w, data, q, s, c, rows, col_begin, col_end, bias=bias, want_dots=want_dots,
+                    fused=fused)
 
 
 @pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
@@ -193,6 +195,26 @@ def test_product_is_bit_exact(fk, dtype, rows):
     assert same_bits(got, want), first_mismatch(got, want)
     got_dots = gpu_product(fk, t, x, rows, dots=True)
     assert np.array_equal(got_dots, want_dots)
+
+
+@pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
+@pytest.mark.parametrize("rows", [1, 4, 5, 16, 33, 100])
+def test_fused_scale_is_the_neon_backends_bits(fk, dtype, rows):
+    """FG_FUSED_SCALE: each group's total scaled with one fused multiply-add in group order (the
+    NEON backend, arch/neon.rs:140-154), bit-exact against the oracle's fused product, bias
+    included; it differs from the scalar backend's bits somewhere."""
+    n_rows, cols = 70, 512
+    data = synthetic_table(dtype, n_rows, cols, seed=40 + rows)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=41 + rows, outliers=0.02)
+    bias = np.random.default_rng(rows).standard_normal(n_rows).astype(np.float32)
+    want = oracle_product(dtype, n_rows, cols, data, x, rows, bias=bias, fused=True)
+    got = gpu_product(fk, t, x, rows, bias=bias, fused_scale=True)
+    assert same_bits(got, want), first_mismatch(got, want)
+    got_pre = gpu_product(fk, t, x, rows, bias=bias, fused=False, fused_scale=True)
+    assert same_bits(got_pre, want)
+    plain = oracle_product(dtype, n_rows, cols, data, x, rows, bias=bias)
+    assert not same_bits(plain, want)
 
 
 @pytest.mark.parametrize("dtype", PRODUCT_FORMATS)

@@ -246,6 +246,45 @@ def test_f32_sum_is_sequential_over_groups_with_unfused_scaling():
     assert mismatched_fma > 0
 
 
+def round_f32(value):
+    """The f32 nearest a rational (ties to even), by exact comparison of the neighbours."""
+    from fractions import Fraction
+    if value == 0:
+        return np.float32(0.0)
+    x = np.float32(float(value))
+    best = None
+    for c in (np.nextafter(x, np.float32(-np.inf)), x, np.nextafter(x, np.float32(np.inf))):
+        key = (abs(Fraction(float(c)) - value), int(np.array(c, np.float32).view(np.uint32)) & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return np.float32(best[1])
+
+
+@pytest.mark.parametrize("dtype", [O.Q8B32, O.Q4B32, O.T2B128])
+def test_fused_scaling_rounds_once_per_group(dtype):
+    """The NEON backend's scaling (arch/neon.rs:140-154), from exact rationals: per group in order,
+    s = round(D·fl(ws·as) + s), one rounding of the exact multiply-add; the separately rounded
+    scalar form differs on these inputs."""
+    from fractions import Fraction
+    rng = np.random.default_rng(17 + dtype)
+    n_rows, cols, rows = 8, O.group(dtype) * 12, 2
+    table = O.encode(dtype, n_rows, cols, rng.standard_normal((n_rows, cols)).astype(np.float32))
+    x = (rng.standard_normal(rows * cols) * np.exp(rng.standard_normal(rows * cols))).astype(np.float32)
+    q, s, c = O.quantize_rows(x, dtype)
+    out, dots = O.matmul(dtype, n_rows, cols, table, q, s, c, rows, want_dots=True, fused=True)
+    plain = O.matmul(dtype, n_rows, cols, table, q, s, c, rows)
+    scales = table[O.quant_len(dtype, n_rows, cols):].view(np.float32)
+    G = cols // O.group(dtype)
+    for r in range(rows):
+        for n in range(n_rows):
+            acc = np.float32(0.0)
+            for g in range(G):
+                p = np.float32(scales[((n // 4) * G + g) * 4 + n % 4] * s[r * G + g])
+                acc = round_f32(Fraction(int(dots[r, n, g])) * Fraction(float(p)) + Fraction(float(acc)))
+            assert out[r, n] == acc, (r, n)
+    assert np.any(out[:, :n_rows] != plain[:, :n_rows])
+
+
 def test_bias_is_added_after_the_sum_and_columns_are_whole_quads():
     rng = np.random.default_rng(9)
     n_rows, cols = 10, 64

@@ -227,21 +227,27 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     }
     long rw[kDepthW], ra[kDepthA];
     float rs[kDepthW];
+    // block by block, in the order the loop refills the ring: waiting for a block's operands then
+    // leaves the younger blocks' loads in flight (vector loads complete in order)
+    static_assert(kDepthA == kDepthW, "one ring");
 #pragma unroll
     for (int k = 0; k < kDepthW; k++) {
         const int bb = min(k, B - 1);
         rw[k] = *reinterpret_cast<const long *>(wrow + size_t(bb) * QB);
         rs[k] = wsrow[size_t(bb) * 4];
+        ra[k] = *reinterpret_cast<const long *>(arow + bb * 32);
+        __builtin_amdgcn_sched_barrier(0);  // the scheduler would otherwise group the loads by array
     }
-#pragma unroll
-    for (int k = 0; k < kDepthA; k++) ra[k] = *reinterpret_cast<const long *>(arow + min(k, B - 1) * 32);
     __builtin_amdgcn_sched_barrier(0);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int b = 0; b < B; b += kDepthW) {
 #pragma unroll
         for (int k = 0; k < kDepthW; k++) {
             const int bb = b + k;
-            if (bb < B) {
+            // no branch around a block but for the dots: past the last block the operands are
+            // clamped re-reads and the term is +0, which leaves the sum (never −0) as it is
+            const bool live = bb < B;
+            if (!DOTS || live) {
                 long w = rw[k];
                 if (FMT == 4) {
                     const int lo = nibbles_signed(int(w) >> shift), hi = nibbles_signed(int(w >> 32) >> shift);
@@ -257,17 +263,19 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
                     }
                 } else {
                     const float ws = rs[k];
-                    const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + bb * 16 + 4 * s);
+                    const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + min(bb, B - 1) * 16 + 4 * s);
+                    const float d0 = live ? float(d[0]) : 0.0f, d1 = live ? float(d[1]) : 0.0f;
+                    const float d2 = live ? float(d[2]) : 0.0f, d3 = live ? float(d[3]) : 0.0f;
                     if (FUSED) {
-                        acc[0] = __builtin_fmaf(float(d[0]), ws * sc.x, acc[0]);
-                        acc[1] = __builtin_fmaf(float(d[1]), ws * sc.y, acc[1]);
-                        acc[2] = __builtin_fmaf(float(d[2]), ws * sc.z, acc[2]);
-                        acc[3] = __builtin_fmaf(float(d[3]), ws * sc.w, acc[3]);
+                        acc[0] = __builtin_fmaf(d0, ws * sc.x, acc[0]);
+                        acc[1] = __builtin_fmaf(d1, ws * sc.y, acc[1]);
+                        acc[2] = __builtin_fmaf(d2, ws * sc.z, acc[2]);
+                        acc[3] = __builtin_fmaf(d3, ws * sc.w, acc[3]);
                     } else {
-                        acc[0] = acc[0] + float(d[0]) * (ws * sc.x);
-                        acc[1] = acc[1] + float(d[1]) * (ws * sc.y);
-                        acc[2] = acc[2] + float(d[2]) * (ws * sc.z);
-                        acc[3] = acc[3] + float(d[3]) * (ws * sc.w);
+                        acc[0] = acc[0] + d0 * (ws * sc.x);
+                        acc[1] = acc[1] + d1 * (ws * sc.y);
+                        acc[2] = acc[2] + d2 * (ws * sc.z);
+                        acc[3] = acc[3] + d3 * (ws * sc.w);
                     }
                 }
             }

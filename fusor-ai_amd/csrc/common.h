@@ -96,27 +96,25 @@ __device__ __forceinline__ int sum8(int v)
     v += xor2(v);
     return v + mirror8(v);
 }
-// Maximum over the wave (NaN ignored, as fmaxf does): groups of 8 through DPP, then the eight
-// group results read out.
-__device__ __forceinline__ float wave_max(float v)
+// Maximum / sum over the wave of a value every lane holds, every lane getting the result: DPP
+// within rows of 16 lanes, then lane exchanges across the rows (no scalar round trips).
+__device__ __forceinline__ float wave_allmax(float v)
 {
-    v = max8(v);
-    float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-#pragma unroll
-    for (int g = 8; g < 64; g += 8) m = fmaxf(m, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), g)));
-    return m;
+    v = fmaxf(v, __int_as_float(xor1(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(xor2(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(mirror8(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));  // row_ror:8
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
 }
-// Sum over the wave, in no particular order: groups of 8 through DPP, then the eight group
-// results read out and added.
-__device__ __forceinline__ float wave_sum_unordered(float v)
+__device__ __forceinline__ float wave_allsum(float v)
 {
     v = v + __int_as_float(xor1(__float_as_int(v)));
     v = v + __int_as_float(xor2(__float_as_int(v)));
     v = v + __int_as_float(mirror8(__float_as_int(v)));
-    float s = 0.0f;
-#pragma unroll
-    for (int g = 0; g < 64; g += 8) s = s + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), g));
-    return s;
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+    v = v + __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
 }
 
 // Activation quantization of one value at scale d (scalar.rs:57-66): ties-to-even rounding of the

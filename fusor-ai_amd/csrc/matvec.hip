@@ -299,7 +299,7 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             FG_SQ(g.f2, 2)
             FG_SQ(g.f3, 3)
 #undef FG_SQ
-            part = wave_sum_unordered(part);
+            part = wave_allsum(part);
             if ((tid & 63) == 0) red[tid >> 6] = part;
             __syncthreads();
             total = ((red[0] + red[1]) + red[2]) + red[3];
@@ -374,27 +374,6 @@ __device__ __forceinline__ void load_kv_tile(const ProjParams &p, int kv, int j0
             t.v[e] = vt[at];
         }
     }
-}
-
-// Maximum / sum over the wave of a value held by every lane (DPP within rows of 16, then lane
-// exchanges across rows).
-__device__ __forceinline__ float wave_allmax(float v)
-{
-    v = fmaxf(v, __int_as_float(xor1(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(xor2(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(mirror8(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));  // row_ror:8
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
-}
-__device__ __forceinline__ float wave_allsum(float v)
-{
-    v = v + __int_as_float(xor1(__float_as_int(v)));
-    v = v + __int_as_float(xor2(__float_as_int(v)));
-    v = v + __int_as_float(mirror8(__float_as_int(v)));
-    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
-    v = v + __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
 }
 
 // Chunk c of query head h: keys [c·per_chunk, min((c + 1)·per_chunk, position)); the first tile is

@@ -41,6 +41,23 @@ struct GemmParams {
     int dots_cols;
 };
 
+// Workgroups in launch order go round-robin to the 8 XCDs, each with its own L2, so neighbouring
+// tiles (which share activation rows or weight columns) would land on different L2s. The tile of
+// launch index L is renumbered so that each XCD takes a contiguous run of tiles, and the runs
+// are laid over the [Y row tiles][X column tiles] grid in groups of kGroupRows row tiles, row
+// tile fastest: the waves resident on one XCD at a time share a few weight columns and a band
+// of activation rows in its L2. A bijection of [0, X·Y).
+constexpr int kGroupRows = 16;
+
+__device__ __forceinline__ void tile_of(int L, int X, int Y, int &tx, int &ty)
+{
+    const int T = X * Y, per = T >> 3, rem = T & 7, xcd = L & 7, j = L >> 3;
+    const int t = xcd < rem ? xcd * (per + 1) + j : rem * (per + 1) + (xcd - rem) * per + j;
+    const int g = t / (kGroupRows * X), rows = min(kGroupRows, Y - g * kGroupRows), in = t - g * kGroupRows * X;
+    ty = g * kGroupRows + in % rows;
+    tx = in / rows;
+}
+
 // One wave per workgroup and per 32 x 32·TN output tile (TN MFMAs per block): enough waves to
 // spread the exact rescale, four VALU operations per output per block and the product's bound,
 // over every SIMD. Operands stream straight from memory, kDepth blocks ahead of the block being
@@ -63,7 +80,9 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     extern __shared__ __align__(16) float tile_scales[];  // [B][32] when LDS_SCALES
     constexpr int QB = FMT == 8 ? 128 : 64;  // device bytes per quad block
     const int lane = threadIdx.x, i = lane & 31, h = lane >> 5;
-    const int m0 = int(blockIdx.y) * 32, n0 = p.col_begin + int(blockIdx.x) * 32 * TN;
+    int tx, ty;
+    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 32 * TN - 1) / (32 * TN), (p.M + 31) / 32, tx, ty);
+    const int m0 = ty * 32, n0 = p.col_begin + tx * 32 * TN;
     const int row = min(m0 + i, p.M - 1);
     const int8_t *arow = p.q + size_t(row) * p.K + h * 16;
     const float *asrow = p.as_t + m0 + 4 * h;
@@ -112,7 +131,24 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
-    auto multiply = [&](int b, const Stage<TN, LDS_SCALES> &st) {
+    // The product of a block (TN MFMAs) is issued one block ahead of its rescale, so that the
+    // matrix cores work on block b + 1 while the VALU scales block b, within one wave.
+    struct Prod {
+        v16i d[TN];
+    };
+    auto product = [&](const Stage<TN, LDS_SCALES> &st, Prod &pr) {
+#pragma unroll
+        for (int t = 0; t < TN; t++) {
+            v4i w = st.w[t];
+            if (FMT == 4) {
+                const int sh = h * 4;
+                w = v4i{nibbles_signed(w.x >> sh), nibbles_signed(w.y >> sh), nibbles_signed(w.z >> sh), nibbles_signed(w.w >> sh)};
+            }
+            const v16i zero = {0};
+            pr.d[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(st.a, w, zero, 0, 0, 0);
+        }
+    };
+    auto rescale = [&](int b, const Stage<TN, LDS_SCALES> &st, const Prod &pr) {
         v4f s0 = st.s0, s1 = st.s1, s2 = st.s2, s3 = st.s3;
         if (LDS_SCALES) {
             const v4f *ls = reinterpret_cast<const v4f *>(tile_scales + b * 32 + 4 * h);
@@ -124,13 +160,7 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
         const float sc[16] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w, s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
 #pragma unroll
         for (int t = 0; t < TN; t++) {
-            v4i w = st.w[t];
-            if (FMT == 4) {
-                const int sh = h * 4;
-                w = v4i{nibbles_signed(w.x >> sh), nibbles_signed(w.y >> sh), nibbles_signed(w.z >> sh), nibbles_signed(w.w >> sh)};
-            }
-            const v16i zero = {0};
-            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(st.a, w, zero, 0, 0, 0);
+            const v16i d = pr.d[t];
             if (DOTS) {
                 const int n = n0 + 32 * t + i;
 #pragma unroll
@@ -148,30 +178,25 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     };
 
     // the ring: block b lives in stage b % kDepth; the fetch of block b + kDepth follows the
-    // multiply of block b (clamped at the last block, so the loop body has no branch around
+    // rescale of block b (clamped at the last block, so the loop body has no branch around
     // loads). Scheduling barriers keep each stage's work below the waits of younger loads.
-    Stage<TN, LDS_SCALES> st0, st1, st2, st3;
-    fetch(0, st0);
-    __builtin_amdgcn_sched_barrier(0);
-    fetch(min(1, B - 1), st1);
-    __builtin_amdgcn_sched_barrier(0);
-    fetch(min(2, B - 1), st2);
-    __builtin_amdgcn_sched_barrier(0);
-    fetch(min(3, B - 1), st3);
-    __builtin_amdgcn_sched_barrier(0);
+    static_assert(kDepth % 2 == 0, "two products in flight alternate with the block's parity");
+    Stage<TN, LDS_SCALES> st[kDepth];
+#pragma unroll
+    for (int k = 0; k < kDepth; k++) {
+        fetch(min(k, B - 1), st[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    Prod pr[2];
+    product(st[0], pr[0]);
     for (int b = 0; b < B; b += kDepth) {
-        multiply(b, st0);
-        fetch(min(b + 4, B - 1), st0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (b + 1 < B) multiply(b + 1, st1);
-        fetch(min(b + 5, B - 1), st1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (b + 2 < B) multiply(b + 2, st2);
-        fetch(min(b + 6, B - 1), st2);
-        __builtin_amdgcn_sched_barrier(0);
-        if (b + 3 < B) multiply(b + 3, st3);
-        fetch(min(b + 7, B - 1), st3);
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < kDepth; k++) {
+            product(st[(k + 1) % kDepth], pr[(k + 1) & 1]);  // block b + k + 1 (a clamped re-read past the end)
+            if (k == 0 || b + k < B) rescale(b + k, st[k], pr[k & 1]);
+            fetch(min(b + k + kDepth, B - 1), st[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     if (DOTS) return;
 #pragma unroll
@@ -204,8 +229,10 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     extern __shared__ __align__(16) float tile_scales[];  // [B][16]
     constexpr int QB = FMT == 8 ? 128 : 64;
     const int lane = threadIdx.x, i = lane & 15, s = lane >> 4;  // s: this lane's slice of 8 inputs
-    const int n0 = p.col_begin + int(blockIdx.x) * 16;
-    const int row = min(i, p.M - 1);
+    int tx, ty;
+    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 15) / 16, (p.M + 15) / 16, tx, ty);
+    const int m0 = ty * 16, n0 = p.col_begin + tx * 16;
+    const int row = min(m0 + i, p.M - 1);
     const int n = n0 + i, nc = min(n, p.col_end - 1);
     const int B = p.B;
     const int8_t *arow = p.q + size_t(row) * p.K + 8 * s;
@@ -258,7 +285,7 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
                 if (DOTS) {
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
-                        const int r = 4 * s + v;
+                        const int r = m0 + 4 * s + v;
                         if (r < p.M && n < p.col_end) p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * p.G + bb] = d[v];
                     }
                 } else {
@@ -289,7 +316,7 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     if (DOTS || n >= p.col_end) return;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-        const int r = 4 * s + v;
+        const int r = m0 + 4 * s + v;
         if (r >= p.M) continue;
         float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
         float y = acc[v];
@@ -312,8 +339,9 @@ template <int FMT, bool FUSED>
 int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
 {
     const int ncols = p.col_end - p.col_begin;
+    const long narrow_waves = long((ncols + 31) / 32) * ((p.M + 31) / 32);
     if (p.M <= 16 && (dots || lds)) {
-        const dim3 grid(unsigned((ncols + 15) / 16));
+        const dim3 grid(unsigned(((ncols + 15) / 16) * ((p.M + 15) / 16)));
         if (dots) gemm16_kernel<FMT, true, false><<<grid, 64, 0, s>>>(p);
         else gemm16_kernel<FMT, false, FUSED><<<grid, 64, size_t(p.B) * 16 * 4, s>>>(p);
         FG_HIP(hipGetLastError());
@@ -322,12 +350,12 @@ int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
     const long wide_waves = long((ncols + 63) / 64) * ((p.M + 31) / 32);
     const size_t smem = size_t(p.B) * 32 * 4;
     if (wide_waves >= 1024) {
-        dim3 grid(unsigned((ncols + 63) / 64), unsigned((p.M + 31) / 32));
+        const dim3 grid{unsigned(wide_waves)};
         if (dots) gemm_kernel<FMT, 2, true, false, false><<<grid, 64, 0, s>>>(p);
         else if (lds) gemm_kernel<FMT, 2, false, true, FUSED><<<grid, 64, smem, s>>>(p);
         else gemm_kernel<FMT, 2, false, false, FUSED><<<grid, 64, 0, s>>>(p);
     } else {
-        dim3 grid(unsigned((ncols + 31) / 32), unsigned((p.M + 31) / 32));
+        const dim3 grid{unsigned(narrow_waves)};
         if (dots) gemm_kernel<FMT, 1, true, false, false><<<grid, 64, 0, s>>>(p);
         else if (lds) gemm_kernel<FMT, 1, false, true, FUSED><<<grid, 64, smem, s>>>(p);
         else gemm_kernel<FMT, 1, false, false, FUSED><<<grid, 64, 0, s>>>(p);

@@ -114,12 +114,14 @@ int launch_matvec(const ProductArgs &a, hipStream_t s)
     if (nq <= 0) return FG_OK;
     const int in = a.x ? IN_F32 : IN_PREQ;
     const int out = a.dots ? OUT_DOTS : OUT_STORE;
-    // Quads per workgroup: about 16 KiB of codes per workgroup, halved while fewer than 128
-    // workgroups would cover the chip, and at most about 2400 workgroups for the largest tables.
+    // Quads per workgroup: the most (a power of two, at most 16) whose codes fit in 64 KiB,
+    // halved while fewer than 128 workgroups would cover the chip. Measured on 4864 x 896 Q8b32
+    // (8 quads: 4.1 us against 4.6 at 4), 14336 x 4096 Q4b32 (8: 10.3 us against 13.1 at 2) and
+    // 151936 x 896 (16).
     const int run = int(t->blocks) * (t->dtype == FG_Q4B32 ? 64 : 128);  // code bytes per quad
-    int qpw = std::max(1, 16384 / run);
+    int qpw = 16;
+    while (qpw > 1 && qpw * run > 65536) qpw /= 2;
     while (qpw > 1 && (nq + qpw - 1) / qpw < 128) qpw /= 2;
-    qpw = std::min(16, std::max(qpw, (nq + 2399) / 2400));
     p.qpw = qpw;
     p.qstride = 1;
     proj_derive(p);

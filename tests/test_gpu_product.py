@@ -197,6 +197,25 @@ def test_product_is_bit_exact(fk, dtype, rows):
     assert np.array_equal(got_dots, want_dots)
 
 
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+@pytest.mark.parametrize("cols", [32, 160])
+def test_wide_tiles_with_ragged_edges_and_short_rings(fk, dtype, cols):
+    """100 rows x 16386 outputs: more than 1024 tiles of 32 x 64, so the product takes the wide
+    tiles in their per-XCD order, with a partial last row tile, a partial last column tile and a
+    padding row; 1 and 5 blocks per row, fewer than and not a multiple of the four-block ring."""
+    rows, n_rows = 100, 16386
+    data = synthetic_table(dtype, n_rows, cols, seed=cols)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=7 + cols, outliers=0.02)
+    want, want_dots = oracle_product(dtype, n_rows, cols, data, x, rows, want_dots=True)
+    got = gpu_product(fk, t, x, rows)
+    assert same_bits(got, want), first_mismatch(got, want)
+    assert np.array_equal(gpu_product(fk, t, x, rows, dots=True), want_dots)
+    want_f = oracle_product(dtype, n_rows, cols, data, x, rows, fused=True)
+    got_f = gpu_product(fk, t, x, rows, fused_scale=True)
+    assert same_bits(got_f, want_f), first_mismatch(got_f, want_f)
+
+
 @pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
 @pytest.mark.parametrize("rows", [1, 4, 5, 16, 33, 100])
 def test_fused_scale_is_the_neon_backends_bits(fk, dtype, rows):

@@ -360,7 +360,7 @@ __device__ __forceinline__ void load_kv_tile(const ProjParams &p, int kv, int j0
 {
     if (D == 0) return;
     using S = AttnShape<D>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, jk = tid >> 2, part = tid & 3;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), jk = tid >> 2, part = tid & 3;
     const size_t row0 = p.layer_base + (size_t(kv) * p.capacity + size_t(j0)) * D;  // the tile's first key
     const float *kt = p.kcache + row0, *vt = p.vcache + row0;
     const unsigned koff = unsigned((jk < n ? jk : 0) * D + part * S::DQ);
@@ -390,7 +390,7 @@ __device__ __forceinline__ void attend_chunk(const ProjParams &p, const float *q
 {
     if (D == 0) return;
     using S = AttnShape<D>;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, jk = tid >> 2, part = tid & 3;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), jk = tid >> 2, part = tid & 3;
     const int kv = divq(h, p.rcp_group);
     const int first = c * p.per_chunk, last = min(p.position, first + p.per_chunk);
     int key0, dim0;
@@ -512,7 +512,9 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     float *terms = reinterpret_cast<float *>(smem + lay.off_terms);  // [NT][R][NW][Gp]
     float *nbuf = reinterpret_cast<float *>(smem + lay.off_n);       // [K] (IN_NORM)
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index in a scalar register: what depends only on it (a wave's chunks, its batch
+    // count, the slots it skips) becomes scalar work and branches rather than per-lane masks
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     constexpr int QB = FMT == 8 ? 128 : 64;         // device bytes per quad block
     constexpr int QB_PER_CHUNK = 1024 / QB;         // quad blocks per 1 KiB chunk
     const int total_qb = nq * B;

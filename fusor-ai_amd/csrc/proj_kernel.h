@@ -76,18 +76,19 @@ __device__ __forceinline__ float ordered_sum(const float *t, int n)
 #pragma unroll
         for (int k = 0; k < V; k++) cur[k] = nxt[k];
     }
-    const int g0 = runs * 4 * V, rest4 = (n - g0 + 3) / 4;
+    const int g0 = runs * 4 * V, rest4 = (n - g0 + 3) / 4;  // uniform
     if (rest4 > 0) {
 #pragma unroll
         for (int k = 0; k < V; k++) cur[k] = t4[runs * V + min(k, rest4 - 1)];
+        // the row is zero-padded to whole float4s, and s is never -0 (it starts at +0), so the
+        // padding's +0 terms change nothing; whole float4s end on a scalar branch
 #pragma unroll
         for (int k = 0; k < V; k++) {
-            // s is never -0 (it starts at +0), so adding +0 for a term past the end is no change
-            const int g = g0 + 4 * k;
-            s = s + (g < n ? cur[k].x : 0.0f);
-            s = s + (g + 1 < n ? cur[k].y : 0.0f);
-            s = s + (g + 2 < n ? cur[k].z : 0.0f);
-            s = s + (g + 3 < n ? cur[k].w : 0.0f);
+            if (k >= rest4) break;
+            s = s + cur[k].x;
+            s = s + cur[k].y;
+            s = s + cur[k].z;
+            s = s + cur[k].w;
         }
     }
     return s;
@@ -678,6 +679,11 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         __builtin_amdgcn_sched_barrier(0);
     }
     stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
+    if (!TREE && OUT != OUT_DOTS && Gp != G) {
+        // term rows zero-padded to whole float4s (the ordered sum reads them whole)
+        for (int i = threadIdx.x; i < NT * R * NW; i += kThreads)
+            for (int g2 = G; g2 < Gp; g2++) terms[i * Gp + g2] = 0.0f;
+    }
     __syncthreads();
     if constexpr (kDouble) {
         for (int b = 0; b < batches; b += 2) {

@@ -198,6 +198,24 @@ def test_product_is_bit_exact(fk, dtype, rows):
 
 
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+@pytest.mark.parametrize("rows", [1, 2, 4])
+@pytest.mark.parametrize("cols", [32, 96, 160, 1184])
+def test_matvec_with_group_counts_not_a_multiple_of_four(fk, dtype, rows, cols):
+    """1, 3, 5 and 37 groups per row: the matrix-vector kernel's rows of group terms are padded
+    to whole float4s, and the group-order sum must stop at the last real group."""
+    n_rows = 37
+    data = synthetic_table(dtype, n_rows, cols, seed=cols + rows)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=3 * cols + rows, outliers=0.02)
+    bias = np.random.default_rng(cols).standard_normal(n_rows).astype(np.float32)
+    want = oracle_product(dtype, n_rows, cols, data, x, rows, bias=bias)
+    got = gpu_product(fk, t, x, rows, bias=bias)
+    assert same_bits(got, want), first_mismatch(got, want)
+    got_pre = gpu_product(fk, t, x, rows, bias=bias, fused=False)
+    assert same_bits(got_pre, want), first_mismatch(got_pre, want)
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
 @pytest.mark.parametrize("cols", [32, 160])
 def test_wide_tiles_with_ragged_edges_and_short_rings(fk, dtype, cols):
     """100 rows x 16386 outputs: more than 1024 tiles of 32 x 64, so the product takes the wide

@@ -68,6 +68,8 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     if (p.qstride > 1 && (nq % span || p.qpw != 2)) return set_error(FG_ERR_SHAPE, "strided quads come in whole pairs");
     if (out == OUT_QKV && (p.qpw != 2 || p.qstride * 8 != p.D))
         return set_error(FG_ERR_SHAPE, "the QKV epilogue takes one rotary pair per workgroup");
+    if (out == OUT_SWIGLU && p.q_out && (p.qpw != 8 || p.qstride != 1 || nq % 8))
+        return set_error(FG_ERR_SHAPE, "the quantized SwiGLU row takes 8 quads (one group) per workgroup");
     if (in == IN_NORM && p.K > 4 * 4 * kThreads) return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
     if (in == IN_ATTN && (p.K > 4 * kThreads || p.chunks < 1 || p.chunks > kMaxChunks || p.heads * p.D != p.K ||
                           (p.D != 32 && p.D != 64 && p.D != 128) || p.kv_heads < 1 || p.heads % p.kv_heads))

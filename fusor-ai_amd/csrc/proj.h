@@ -58,8 +58,13 @@ struct ProjParams {
     float *kcache, *vcache;
     size_t layer_base;
     int capacity, position;
-    // SwiGLU epilogue: silu(gate)·up, f32 (the down projection quantizes it in its prologue)
+    // SwiGLU epilogue: silu(gate)·up, f32 (when set)
     float *act_out;
+    // OUT_SWIGLU with 8 quads per workgroup (32 outputs, one group of 32): the row also quantized
+    // per group (quantize_rows' levels, scales and corrections), when q_out is set
+    int8_t *q_out;
+    float *s_out;
+    int32_t *c_out;
     // OUT_QATTN: workgroup w < heads·chunks projects query head w / chunks (its D rows) and attends
     // over keys [c·per_chunk, min((c + 1)·per_chunk, position)) of chunk c = w % chunks, writing the
     // chunk's record to `states`; the rest project the key and value rows in rotary pairs

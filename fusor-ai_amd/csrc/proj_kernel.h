@@ -832,7 +832,20 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         }
     } else if (OUT == OUT_SWIGLU) {
         // silu(gate)·up (layer.rs:321-341); the down projection quantizes the row
-        for (int nl = threadIdx.x; nl < nq * 4; nl += kThreads) p.act_out[output_of(nl)] = ref_silu(ybuf[nl]) * ybuf[NW + nl];
+        for (int nl = threadIdx.x; nl < nq * 4; nl += kThreads) {
+            const float y = ref_silu(ybuf[nl]) * ybuf[NW + nl];
+            if (p.act_out) p.act_out[output_of(nl)] = y;
+            ybuf[nl] = y;  // in place of the gate: slot nl is this thread's alone
+        }
+        if (p.q_out && wave == 0) {
+            // the workgroup's 32 outputs are one group (written above by lanes 0..31 of this
+            // wave): lanes 0..7 take four consecutive products each and quantize them as the
+            // next projection's prologue would (the other lanes' groups are not stored)
+            const v4f v[1] = {*reinterpret_cast<const v4f *>(ybuf + 4 * (lane & 7))};
+            Group8 gr[1];
+            quantize_groups<1>(v, gr);
+            if (lane < 8) store_group8(gr[0], p.zp, output_of(0) / 32, p.q_out, p.s_out, p.c_out);
+        }
     }
 }
 

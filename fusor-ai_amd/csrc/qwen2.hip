@@ -9,7 +9,8 @@
 //      then softmax and weighted values by head and 32 value dimensions, quantized for the output
 //      projection
 //   3. output projection added to the residual row
-//   4. RMSNorm + quantize -> gate and up products -> silu(gate)·up quantized for down
+//   4. RMSNorm + quantize -> gate and up products -> silu(gate)·up, each workgroup's 32 outputs
+//      quantized as one group for down
 //   5. down projection added to the residual row
 // In parallel order, four: 1 and 2 become one launch whose workgroups each project one query head
 // and attend over one chunk of the cached keys (flash decoding), next to workgroups projecting the
@@ -313,7 +314,6 @@ struct fg_qwen2 {
     float *kcache, *vcache;
     // activations
     float *hidden, *qkv, *logits, *rope;  // rope: [capacity][cos | sin]
-    float *ffn;                           // silu(gate)·up, [ffn]
     int8_t *xq;
     float *xs;
     int32_t *xc;
@@ -409,15 +409,13 @@ int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t positi
 
 // 3. and 5. a projection added to the residual row: of the attention's output (o: quantized by
 // the attention, or merged from its chunks and the new key and quantized in the prologue), or of
-// the f32 silu(gate)·up row, quantized in the prologue (down).
+// the silu(gate)·up row quantized by the SwiGLU epilogue (down).
 int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st, size_t li = 0, size_t position = 0)
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(t);
     p.qpw = 1;
-    if (in == IN_F32) {
-        p.x = m->ffn;
-    } else if (in == IN_ATTN) {
+    if (in == IN_ATTN) {
         p.part = m->part;
         p.chunks = m->chunks;
         p.heads = int(sh.heads);
@@ -448,12 +446,14 @@ int swiglu_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, hipStream_t st)
     ProjParams p = table_params(ly.gate);
     p.codes2 = ly.up->codes;
     p.wscales2 = ly.up->scales;
-    p.qpw = 2;
+    p.qpw = 8;  // 32 outputs per workgroup: one group of the row, quantized in the epilogue
     p.x = m->hidden;
     p.norm_w = ly.norm2;
     p.eps = sh.eps;
     p.zp = m->zp;
-    p.act_out = m->ffn;
+    p.q_out = m->xq;
+    p.s_out = m->xs;
+    p.c_out = m->xc;
     return launch_proj(p, sh.dtype, IN_NORM, OUT_SWIGLU, sh.exact != 0, st);
 }
 
@@ -498,7 +498,7 @@ int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
         if ((rc = residual_launch(m, ly.o, IN_PREQ, st))) return rc;
     }
     if ((rc = swiglu_launch(m, ly, st))) return rc;
-    return residual_launch(m, ly.down, IN_F32, st);
+    return residual_launch(m, ly.down, IN_PREQ, st);
 }
 
 int head_launch(fg_qwen2 *m, hipStream_t st)
@@ -576,7 +576,6 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
     } allocs[] = {
         {reinterpret_cast<void **>(&m->hidden), sh.hidden * 4},
         {reinterpret_cast<void **>(&m->qkv), (qkv_w + 3) / 4 * 4 * 4},
-        {reinterpret_cast<void **>(&m->ffn), sh.ffn * 4},
         {reinterpret_cast<void **>(&m->logits), padded_vocab * 4},
         {reinterpret_cast<void **>(&m->rope), sh.capacity * sh.head_dim * 4},
         {reinterpret_cast<void **>(&m->xq), widest},
@@ -658,7 +657,7 @@ extern "C" int fg_qwen2_step(fg_qwen2 *m, int token, size_t position, float *hid
 extern "C" int fg_qwen2_free(fg_qwen2 *m)
 {
     if (!m) return FG_OK;
-    void *ptrs[] = {m->hidden, m->qkv, m->ffn, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores, m->part};
+    void *ptrs[] = {m->hidden, m->qkv, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores, m->part};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     delete m;

@@ -666,8 +666,17 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     __builtin_amdgcn_sched_barrier(0);
     load(wa, sa);  // every wave, in bounds even without chunks of its own
     __builtin_amdgcn_sched_barrier(0);  // and all of them issued before the prologue's first wait
-    // OUT_QATTN: the first tile of the chunk's cached keys and values, behind the weights (every
-    // workgroup loads one, in bounds, so that no branch splits the loads)
+    stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
+    if (!TREE && OUT != OUT_DOTS && Gp != G) {
+        // term rows zero-padded to whole float4s (the ordered sum reads them whole)
+        for (int i = threadIdx.x; i < NT * R * NW; i += kThreads)
+            for (int g2 = G; g2 < Gp; g2++) terms[i * Gp + g2] = 0.0f;
+    }
+    __syncthreads();
+    // OUT_QATTN: the first tile of the chunk's cached keys and values, issued once the prologue
+    // is done (a wave issues its loads one after another, and the prologue waits behind every
+    // load issued before it) and behind the weights, so it arrives while the query rows are
+    // computed. Every workgroup loads one, in bounds, so that no branch splits the loads.
     KVTile<HD> tile;
     int head = 0, chunk = 0;
     if (OUT == OUT_QATTN) {
@@ -678,13 +687,6 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         load_kv_tile<HD>(p, divq(head, p.rcp_group), first, max(0, min(kTileKeys, min(p.position, first + p.per_chunk) - first)), tile);
         __builtin_amdgcn_sched_barrier(0);
     }
-    stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
-    if (!TREE && OUT != OUT_DOTS && Gp != G) {
-        // term rows zero-padded to whole float4s (the ordered sum reads them whole)
-        for (int i = threadIdx.x; i < NT * R * NW; i += kThreads)
-            for (int g2 = G; g2 < Gp; g2++) terms[i * Gp + g2] = 0.0f;
-    }
-    __syncthreads();
     if constexpr (kDouble) {
         for (int b = 0; b < batches; b += 2) {
             if (b + 1 < batches) load(wb, sb);

@@ -254,17 +254,26 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         for (int c = 0; c < kMaxChunks; c++)
             if (c < p.chunks) M = fmaxf(M, g.pm[c]);
         const float en = ref_exp(sn - M);
+        // e^(m_c − M) once per head: lane c of the head's D/4 lanes (at least 8) takes chunk c,
+        // and every lane of the head reads them back in chunk order
+        const int head0 = (tid & 63) & ~((p.D >> 2) - 1);
+        float mine = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kMaxChunks; c++)
+            if ((tid & 63) - head0 == c) mine = g.pm[c];
+        const float e_mine = (tid & 63) - head0 < p.chunks ? ref_exp(mine - M) : 0.0f;
         float L = en;
         v4f o = g.vn * en;
 #pragma unroll
         for (int c = 0; c < kMaxChunks; c++) {
+            const float e = __shfl(e_mine, head0 + c, 64);
             if (c < p.chunks) {
-                const float e = ref_exp(g.pm[c] - M);
                 L = L + g.pl[c] * e;
                 o = o + g.pa[c] * e;
             }
         }
-        const v4f merged[1] = {o / L};
+        const float inv_L = 1.0f / L;
+        const v4f merged[1] = {o * inv_L};
         quantize_slots<1>(merged, K / 4, p.zp, act_q, act_s, act_c);
     } else {
         // rms_norm (ops.rs:7-16): mean of squares, 1/sqrt(mean + eps), x·inverse·weight; then the

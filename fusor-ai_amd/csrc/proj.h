@@ -102,7 +102,7 @@ __host__ __device__ inline ProjLayout proj_layout(int R, int K, int G, int NW, i
     l.off_red = l.off_c + align16(R * G * 4);
     l.off_y = l.off_red + 16 * 4;
     l.off_terms = l.off_y + align16(ny * R * NW * 4);
-    l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * NW * ((G + 3) & ~3) * 4));
+    l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * NW * ((G + 3) & ~3) * 4 + 4));  // + a spare slot
     l.off_att = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);  // the exact RMSNorm's row
     // OUT_QATTN: the rotated query [NW = D], the waves' maxima and totals [8] and weighted sums [4][D]
     l.total = l.off_att + (out == OUT_QATTN ? align16((NW + 8 + 4 * NW) * 4) : 0);

@@ -546,19 +546,25 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     // division up front, then a quotient and a remainder step.
     const int qb0 = wt * QB_PER_CHUNK + qb_in_chunk;
     const int step_q = stride * QB_PER_CHUNK / B, step_r = stride * QB_PER_CHUNK - step_q * B;
+    // ti: the lane's term slot (ql·4 + L)·Gp + blk in the first table's first row, kept in step
     struct Cursor {
-        int ql, blk;
+        int ql, blk, ti;
     };
+    const int step_t = step_q * 4 * Gp + step_r, wrap_t = 4 * Gp - B;
     auto advance = [&](Cursor &cu) {
         cu.ql += step_q;
         cu.blk += step_r;
+        cu.ti += step_t;
         if (cu.blk >= B) {
             cu.blk -= B;
             cu.ql++;
+            cu.ti += wrap_t;
         }
     };
     const int ql0 = divq(qb0, p.rcp_B);
-    Cursor ccur{ql0, qb0 - ql0 * B};
+    Cursor ccur{ql0, qb0 - ql0 * B, (ql0 * 4 + L) * Gp + (qb0 - ql0 * B)};
+    // the term slot of a quad block past the run's end (its store lands there, never read)
+    const int spare = NT * R * NW * Gp;
 
     // The workgroup's quad blocks, numbered ql·B + blk, sit contiguously from its first quad, but
     // for a strided pair (qs > 1, two quads) whose second half starts (qs − 1)·B blocks later.
@@ -589,7 +595,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     auto consume = [&](int b, const int4 *w, const float *ws) {
 #pragma unroll
         for (int u0 = 0; u0 < kBatch; u0 += U) {
-            int qls[U], blks[U];
+            int qls[U], blks[U], tis[U];
             int4 a0[U][R], a1[U][R];
             float asc[U][R];
             int acr[U][R];
@@ -597,6 +603,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             for (int v = 0; v < U; v++) {
                 qls[v] = ccur.ql;
                 blks[v] = ccur.blk;
+                tis[v] = ccur.ti;
                 advance(ccur);
                 const int blk = blks[v];  // < B always: every read is in bounds
 #pragma unroll
@@ -629,14 +636,16 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
                                                   (w[u].z >> 4) & 0x0F0F0F0F, (w[u].w >> 4) & 0x0F0F0F0F);
                         D = dot16(lo, a0[v][r]) + dot16(hi, a1[v][r]) + acr[v][r];
                     }
-                    if (valid && h == 0) {
-                        if (OUT == OUT_DOTS) {
+                    if (OUT == OUT_DOTS) {
+                        if (valid && h == 0) {
                             const int n = (base + ql * qs) * 4 + L;
                             p.dots[(size_t(r) * p.dots_cols + (n - p.col_begin)) * G + blk] = D;
-                        } else {
-                            const float scale = ws[u] * asc[v][r];
-                            terms[((tb * R + r) * NW + ql * 4 + L) * Gp + blk] = float(D) * scale;
                         }
+                    } else {
+                        // both lanes of a pair hold the same total and scale, so both store the
+                        // same term; a block past the run's end stores to the spare slot
+                        const float scale = ws[u] * asc[v][r];
+                        terms[valid ? tis[v] + (tb * R + r) * NW * Gp : spare] = float(D) * scale;
                     }
                 }
             }

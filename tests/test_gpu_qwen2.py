@@ -156,6 +156,37 @@ def test_layer_forward_equals_the_oracle_layer(fk):
     assert same_bits(host(h), want)
 
 
+@pytest.mark.parametrize("exact", [True, False])
+def test_consecutive_steps_feed_back_the_greedy_token(fk, exact):
+    """Several steps on one model, each fed the previous step's greedy token: the head's last
+    workgroup picks the token and resets its count for the next step. Exact mode matches the
+    oracle's tokens and cache rows step by step; parallel order repeats its own first step."""
+    import torch
+    dtype = O.Q7B32
+    shape = dict(SMALL, vocab=600)  # 150 quads: 10 workgroups of candidates
+    sh, lys, final, table, kc, vc = build(dtype, seed=8, synthetic=False, **shape)
+    model, kd, vd = gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact)
+    oracle = O.Qwen2(sh, lys, final, table)
+    k2, v2 = kc.copy(), vc.copy()
+    nxt = torch.empty(1, dtype=torch.int32, device="cuda")
+    token = 5
+    firsts = []
+    for position in range(4, 9):
+        model.step(token, position, next_token=nxt)
+        got = int(host(nxt)[0])
+        _, _, want = oracle.step(k2, v2, token, position, threads=8)
+        if exact:
+            assert got == want, position
+        firsts.append(got)
+        token = want
+    if exact:
+        assert same_bits(host(kd), k2) and same_bits(host(vd), v2)
+    else:
+        again, _, _ = gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact)
+        again.step(5, 4, next_token=nxt)
+        assert int(host(nxt)[0]) == firsts[0]
+
+
 def test_decoder_rejects_positions_past_the_cache(fk):
     import torch
     dtype = O.Q7B32

@@ -663,7 +663,11 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     // Who sums which output: one thread per output, or (TREE) a team of `team` lanes per output.
     const int outs = NT * R * NW;
     // the largest power of two (at most 64) with outs·team <= 256: no loop ahead of the loads
-    const int team = TREE ? min(64, int(0x80000000u >> __builtin_clz(unsigned(max(1, kThreads / outs))))) : 1;
+    // and no more lanes than the output's float4 runs of terms (the rest would add zeros)
+    const int runs4 = Gp / 4;
+    const int team = TREE ? min(min(64, int(0x80000000u >> __builtin_clz(unsigned(max(1, kThreads / outs))))),
+                                runs4 <= 1 ? 1 : int(2u << (31 - __builtin_clz(unsigned(runs4 - 1)))))
+                          : 1;
     const int my_out = TREE ? int(threadIdx.x) >> __builtin_ctz(unsigned(team)) : int(threadIdx.x);
     const int sub = int(threadIdx.x) - my_out * team;
     // the residual row this workgroup adds to, read early (linear.rs:139-142); read whether or not

@@ -266,38 +266,33 @@ __global__ __launch_bounds__(1024) void greedy_kernel(const float *__restrict__ 
 {
     __shared__ float bv[16];
     __shared__ int bi[16];
+    const float first = logits[0];  // read at once, beside the candidates
     float best = 0.0f;
     int idx = -1;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const int ci = pidx[i];
-        const float cv = pval[i];
-        if (ci >= 0 && (idx < 0 || cv > best || (cv == best && ci < idx))) {
-            best = cv;
-            idx = ci;
-        }
-    }
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = __shfl_xor(best, m, 64);
-        const int oi = __shfl_xor(idx, m, 64);
+    auto take = [&](float ob, int oi) {
         if (oi >= 0 && (idx < 0 || ob > best || (ob == best && oi < idx))) {
             best = ob;
             idx = oi;
         }
-    }
+    };
+    for (int i = threadIdx.x; i < n; i += blockDim.x) take(pval[i], pidx[i]);
+    for (int m = 32; m >= 1; m >>= 1) take(__shfl_xor(best, m, 64), __shfl_xor(idx, m, 64));
     if ((threadIdx.x & 63) == 0) {
         bv[threadIdx.x >> 6] = best;
         bi[threadIdx.x >> 6] = idx;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < int(blockDim.x >> 6); w++) {
-            if (bi[w] >= 0 && (idx < 0 || bv[w] > best || (bv[w] == best && bi[w] < idx))) {
-                best = bv[w];
-                idx = bi[w];
-            }
+    if (threadIdx.x < 64) {
+        // the waves' candidates, one per lane, reduced across the lanes
+        const int waves = int(blockDim.x >> 6);
+        best = 0.0f;
+        idx = -1;
+        if (int(threadIdx.x) < waves) {
+            best = bv[threadIdx.x];
+            idx = bi[threadIdx.x];
         }
-        const float first = logits[0];
-        *out = (first != first || idx < 0) ? 0 : idx;
+        for (int m = 8; m >= 1; m >>= 1) take(__shfl_xor(best, m, 64), __shfl_xor(idx, m, 64));
+        if (threadIdx.x == 0) *out = (first != first || idx < 0) ? 0 : idx;
     }
 }
 

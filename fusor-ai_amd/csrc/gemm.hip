@@ -17,6 +17,9 @@
 // lane l holds column l % 32, rows 8·(v/4) + 4·(l/32) + v%4 for v = 0..15.
 #include "common.h"
 
+#include <cstdint>
+#include <mutex>
+
 namespace fg {
 namespace {
 
@@ -413,6 +416,38 @@ __global__ __launch_bounds__(256) void t2_product_kernel(const uint8_t *__restri
 
 }  // namespace
 
+// Workspaces come from a stream-ordered pool per device that keeps freed memory for the next
+// product: the device's default pool hands it back to the driver at synchronizations, and a new
+// allocation then costs more than a large product. The pools live as long as the process.
+hipError_t workspace_alloc(void **ptr, size_t bytes, hipStream_t s)
+{
+    static std::mutex mu;
+    static hipMemPool_t pools[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipMallocAsync(ptr, bytes, s);
+    hipMemPool_t pool = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!pools[dev]) {
+            hipMemPoolProps props{};
+            props.allocType = hipMemAllocationTypePinned;
+            props.location.type = hipMemLocationTypeDevice;
+            props.location.id = dev;
+            e = hipMemPoolCreate(&pools[dev], &props);
+            if (e != hipSuccess) {
+                pools[dev] = nullptr;
+                return e;
+            }
+            uint64_t keep = UINT64_MAX;
+            (void)hipMemPoolSetAttribute(pools[dev], hipMemPoolAttrReleaseThreshold, &keep);
+        }
+        pool = pools[dev];
+    }
+    return hipMallocFromPoolAsync(ptr, bytes, pool, s);
+}
+
 int launch_t2(const ProductArgs &a, hipStream_t s)
 {
     const fg_table *t = a.t;
@@ -425,7 +460,7 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
     int rc = FG_OK;
     if (a.x) {  // quantize the f32 rows first (groups of 128)
         const size_t qb = (size_t(M) * K + 255) / 256 * 256, sb = (size_t(M) * G * 4 + 255) / 256 * 256;
-        FG_HIP(hipMallocAsync(&ws, qb + 2 * sb, s));
+        FG_HIP(workspace_alloc(&ws, qb + 2 * sb, s));
         q = static_cast<int8_t *>(ws);
         float *sc = reinterpret_cast<float *>(static_cast<char *>(ws) + qb);
         int32_t *co = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + qb + sb);
@@ -464,7 +499,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
     const size_t s_bytes = a.x ? (size_t(M) * G * 4 + 255) / 256 * 256 : 0;
     const size_t t_bytes = (lds || dots) ? 0 : size_t(G) * Mpad * 4;
     void *ws = nullptr;
-    if (q_bytes + s_bytes + t_bytes) FG_HIP(hipMallocAsync(&ws, q_bytes + 2 * s_bytes + t_bytes, s));
+    if (q_bytes + s_bytes + t_bytes) FG_HIP(workspace_alloc(&ws, q_bytes + 2 * s_bytes + t_bytes, s));
     int8_t *q = const_cast<int8_t *>(a.q);
     const float *as = a.as;
     char *base = static_cast<char *>(ws);

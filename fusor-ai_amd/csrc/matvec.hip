@@ -70,7 +70,10 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
         return set_error(FG_ERR_SHAPE, "the QKV epilogue takes one rotary pair per workgroup");
     if (out == OUT_SWIGLU && p.q_out && (p.qpw != 8 || p.qstride != 1 || nq % 8))
         return set_error(FG_ERR_SHAPE, "the quantized SwiGLU row takes 8 quads (one group) per workgroup");
-    if (in == IN_NORM && p.K > 4 * 4 * kThreads) return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
+    if ((in == IN_NORM || in == IN_EMBED) && p.K > 4 * 4 * kThreads)
+        return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
+    if (in == IN_EMBED && (out != OUT_QATTN || !p.e_codes || !p.e_scales || !p.x_out || p.e_lane < 0 || p.e_lane > 3))
+        return set_error(FG_ERR_ARG, "a table row as input takes the query attention, its quad's codes and scales and an output row");
     if (in == IN_ATTN && (p.K > 4 * kThreads || p.chunks < 1 || p.chunks > kMaxChunks || p.heads * p.D != p.K ||
                           (p.D != 32 && p.D != 64 && p.D != 128) || p.kv_heads < 1 || p.heads % p.kv_heads))
         return set_error(FG_ERR_SHAPE, "the attention merge takes rows of at most 1024, head_dim 32/64/128 and 1 to 8 chunks");
@@ -85,7 +88,7 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     const size_t smem = proj_smem(p, 1, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
     const int nb = batch_depth(p, dtype, out);
-    if (out == OUT_QATTN && (in != IN_NORM || exact))  // the parallel-order attention's
+    if (out == OUT_QATTN && ((in != IN_NORM && in != IN_EMBED) || exact))  // the parallel-order attention's
         return set_error(FG_ERR_SHAPE, "the query attention takes a normed row in parallel order");
     return dtype == FG_Q4B32 ? launch_proj_q4(p, in, out, exact, nb, smem, grid, s)
                              : launch_proj_q8(p, in, out, exact, nb, smem, grid, s);

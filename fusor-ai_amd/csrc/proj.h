@@ -9,7 +9,7 @@ namespace fg {
 // Input of a projection: rows already quantized, f32 rows quantized in-kernel, one f32 row
 // RMS-normalized then quantized in-kernel (rms_norm, ops.rs:7-16), or the attention's output row
 // merged from per-chunk softmax states, then quantized.
-constexpr int IN_PREQ = 0, IN_F32 = 1, IN_NORM = 2, IN_ATTN = 3;
+constexpr int IN_PREQ = 0, IN_F32 = 1, IN_NORM = 2, IN_ATTN = 3, IN_EMBED = 4;
 // Chunks of keys per query head in the fast attention; the output projection merges them.
 constexpr int kMaxChunks = 8;
 constexpr int kTileKeys = 64;  // keys per tile of the fast attention
@@ -37,6 +37,13 @@ struct ProjParams {
     const int32_t *corr;
     int zp;
     const float *norm_w;
+    // IN_EMBED: RMSNorm of a table row (Buffers::embed_row, lm.rs:99-107), dequantized in the
+    // prologue from the row's quad (its codes and scales) and lane; workgroup 0 also stores the
+    // row to x_out
+    const int8_t *e_codes;
+    const float *e_scales;
+    int e_lane;
+    float *x_out;
     float eps;
     // IN_ATTN: per (head, chunk) records of D + 4 floats (max, total, -, -, sums), merged with the
     // new key's own state (rotated query in qkv_out, key and value at the position in the caches)
@@ -103,7 +110,7 @@ __host__ __device__ inline ProjLayout proj_layout(int R, int K, int G, int NW, i
     l.off_y = l.off_red + 16 * 4;
     l.off_terms = l.off_y + align16(ny * R * NW * 4);
     l.off_n = l.off_terms + (out == OUT_DOTS ? 0 : align16(NT * R * NW * ((G + 3) & ~3) * 4 + 4));  // + a spare slot
-    l.off_att = l.off_n + (in == IN_NORM ? align16(K * 4) : 0);  // the exact RMSNorm's row
+    l.off_att = l.off_n + (in == IN_NORM || in == IN_EMBED ? align16(K * 4) : 0);  // the exact RMSNorm's row
     // OUT_QATTN: the rotated query [NW = D], the waves' maxima and totals [8] and weighted sums [4][D]
     l.total = l.off_att + (out == OUT_QATTN ? align16((NW + 8 + 4 * NW) * 4) : 0);
     return l;

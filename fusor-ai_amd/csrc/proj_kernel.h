@@ -111,7 +111,7 @@ struct StageRegs {
 };
 
 
-template <int R, int IN>
+template <int FMT, int R, int IN>
 __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
 {
     const int tid = threadIdx.x;
@@ -157,6 +157,30 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
             g.pl[c] = rec[1];
             g.pa[c] = *reinterpret_cast<const v4f *>(rec + 4 + d4);
         }
+    } else if (IN == IN_EMBED) {
+        // float4 i of the table row: four codes of block i / 8 as one dword (Q7/Q8 bytes
+        // 4·(i % 8) ..; Q4 the nibbles of bytes 4·(i % 4) .. at shift 4·((i % 8) / 4)), and the
+        // block's scale
+        const int n4 = K / 4;
+        const int *c4 = reinterpret_cast<const int *>(p.e_codes);
+        const int rowdw = FMT == 8 ? 8 : 4;  // dwords of a row-block
+        auto at = [&](int i) { return unsigned((i >> 3) * (4 * rowdw) + p.e_lane * rowdw + (FMT == 8 ? (i & 7) : (i & 3))); };
+        auto sc = [&](int i) { return unsigned((i >> 3) * 4 + p.e_lane); };
+        const int i0 = min(tid, n4 - 1), i1 = min(tid + kThreads, n4 - 1), i2 = min(tid + 2 * kThreads, n4 - 1),
+                  i3 = min(tid + 3 * kThreads, n4 - 1);
+        g.c0 = c4[at(i0)];
+        g.c1 = c4[at(i1)];
+        g.c2 = c4[at(i2)];
+        g.c3 = c4[at(i3)];
+        g.s0 = p.e_scales[sc(i0)];
+        g.s1 = p.e_scales[sc(i1)];
+        g.s2 = p.e_scales[sc(i2)];
+        g.s3 = p.e_scales[sc(i3)];
+        const v4f *w4 = reinterpret_cast<const v4f *>(p.norm_w);
+        g.w0 = w4[unsigned(i0)];
+        g.w1 = w4[unsigned(i1)];
+        g.w2 = w4[unsigned(i2)];
+        g.w3 = w4[unsigned(i3)];
     } else {
         // one row of at most 4 · 256 float4s (K <= 4096, checked on the host)
         const v4f *x4 = reinterpret_cast<const v4f *>(p.x);
@@ -196,7 +220,7 @@ __device__ __forceinline__ void quantize_slots(const v4f (&v)[S], int n4, int zp
     }
 }
 
-template <int R, int IN, bool EXACT>
+template <int FMT, int R, int IN, bool EXACT>
 __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageRegs &g, int8_t *act_q, float *act_s,
                                              int32_t *act_c, float *nbuf, float *red)
 {
@@ -280,13 +304,28 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         // quantization of the normed row. Thread t holds float4s t, t + 256, ... of the row, so
         // eight consecutive threads hold one group of 32.
         const int n4 = K / 4;
+        v4f f[4] = {g.f0, g.f1, g.f2, g.f3};
+        if (IN == IN_EMBED) {
+            // Matrix::dequantize_row (tensor.rs:247-271): scale · (float)level; workgroup 0 keeps
+            // the row for the residual
+            const int cw[4] = {g.c0, g.c1, g.c2, g.c3};
+            const float cs[4] = {g.s0, g.s1, g.s2, g.s3};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = tid + k * kThreads;
+                const int lv = FMT == 8 ? cw[k] : nibbles_signed(cw[k] >> (((min(i, n4 - 1) & 7) >> 2) * 4));
+                f[k] = v4f{cs[k] * float(int8_t(lv)), cs[k] * float(int8_t(lv >> 8)), cs[k] * float(int8_t(lv >> 16)),
+                           cs[k] * float(int8_t(lv >> 24))};
+                if (blockIdx.x == 0 && i < n4) reinterpret_cast<v4f *>(p.x_out)[i] = f[k];
+            }
+        }
         float total;
         if (EXACT) {
             v4f *row = reinterpret_cast<v4f *>(nbuf);
-            if (tid < n4) row[tid] = g.f0;
-            if (tid + kThreads < n4) row[tid + kThreads] = g.f1;
-            if (tid + 2 * kThreads < n4) row[tid + 2 * kThreads] = g.f2;
-            if (tid + 3 * kThreads < n4) row[tid + 3 * kThreads] = g.f3;
+            if (tid < n4) row[tid] = f[0];
+            if (tid + kThreads < n4) row[tid + kThreads] = f[1];
+            if (tid + 2 * kThreads < n4) row[tid + 2 * kThreads] = f[2];
+            if (tid + 3 * kThreads < n4) row[tid + 3 * kThreads] = f[3];
             __syncthreads();
             if (tid == 0) {
                 float s = -0.0f;  // dot_f32(row, row) in index order (arch/scalar.rs:340-342)
@@ -310,10 +349,10 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             float part = 0.0f;
 #define FG_SQ(v, k) \
     if (tid + (k) * kThreads < n4) part = part + (((v).x * (v).x + (v).y * (v).y) + ((v).z * (v).z + (v).w * (v).w));
-            FG_SQ(g.f0, 0)
-            FG_SQ(g.f1, 1)
-            FG_SQ(g.f2, 2)
-            FG_SQ(g.f3, 3)
+            FG_SQ(f[0], 0)
+            FG_SQ(f[1], 1)
+            FG_SQ(f[2], 2)
+            FG_SQ(f[3], 3)
 #undef FG_SQ
             part = wave_allsum(part);
             if ((tid & 63) == 0) red[tid >> 6] = part;
@@ -321,7 +360,7 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
             total = ((red[0] + red[1]) + red[2]) + red[3];
         }
         const float inverse = 1.0f / sqrtf(total / float(K) + p.eps);
-        const v4f normed[4] = {g.f0 * inverse * g.w0, g.f1 * inverse * g.w1, g.f2 * inverse * g.w2, g.f3 * inverse * g.w3};
+        const v4f normed[4] = {f[0] * inverse * g.w0, f[1] * inverse * g.w1, f[2] * inverse * g.w2, f[3] * inverse * g.w3};
         quantize_slots<4>(normed, n4, p.zp, act_q, act_s, act_c);
     }
 }
@@ -665,7 +704,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     int4 wa[kBatch], wb[kSecond];
     float sa[kBatch], sb[kSecond];
     StageRegs g;
-    stage_issue<R, IN>(p, g);
+    stage_issue<FMT, R, IN>(p, g);
     // Who sums which output: one thread per output, or (TREE) a team of `team` lanes per output.
     const int outs = NT * R * NW;
     // the largest power of two (at most 64) with outs·team <= 256: no loop ahead of the loads
@@ -694,7 +733,7 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
     __builtin_amdgcn_sched_barrier(0);
     load(wa, sa, kSplit ? 0 : -1);  // every wave, in bounds even without chunks of its own
     __builtin_amdgcn_sched_barrier(0);  // and all of them issued before the prologue's first wait
-    stage_finish<R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
+    stage_finish<FMT, R, IN, EXACT>(p, g, act_q, act_s, act_c, nbuf, red);
     if (!TREE && OUT != OUT_DOTS && Gp != G) {
         // term rows zero-padded to whole float4s (the ordered sum reads them whole)
         for (int i = threadIdx.x; i < NT * R * NW; i += kThreads)

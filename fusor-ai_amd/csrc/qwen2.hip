@@ -370,7 +370,7 @@ bool fast_attention(const fg_qwen2 *m) { return !m->shape.exact && m->shape.head
 // bias -> RoPE) recomputed by each of its chunk workgroups, which then attend over their chunk of
 // the cached keys [0, position); the key and value rows of the position projected, rotated and
 // kept by the remaining workgroups. The output projection merges the chunks with the new key.
-int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position, hipStream_t st)
+int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position, hipStream_t st, int token = -1)
 {
     const fg_qwen2_shape &sh = m->shape;
     // chunks of whole tiles over the cached keys, at most kMaxChunks per head (at least one)
@@ -399,6 +399,17 @@ int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t positi
     p.chunks = m->chunks;
     p.per_chunk = m->per_chunk;
     p.states = m->part;
+    if (token >= 0) {
+        // the first layer reads the token's table row itself (Buffers::embed_row, lm.rs:99-107)
+        // and keeps it in hidden for the residual
+        const fg_table *t = m->table;
+        const size_t quad = size_t(token) / 4, qbytes = t->dtype == FG_Q4B32 ? 64 : 128;
+        p.e_codes = t->codes + quad * t->blocks * qbytes;
+        p.e_scales = t->scales + quad * t->groups * 4;
+        p.e_lane = token % 4;
+        p.x_out = m->hidden;
+        return launch_proj(p, sh.dtype, IN_EMBED, OUT_QATTN, false, st);
+    }
     return launch_proj(p, sh.dtype, IN_NORM, OUT_QATTN, false, st);
 }
 
@@ -480,12 +491,13 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     return FG_OK;
 }
 
-int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
+// token >= 0: the layer's input is that table row (the first layer of a step in parallel order)
+int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st, int token = -1)
 {
     const fg_qwen2_layer &ly = m->layers[li];
     int rc;
     if (fast_attention(m)) {
-        if ((rc = qattn_launch(m, ly, li, position, st))) return rc;
+        if ((rc = qattn_launch(m, ly, li, position, st, token))) return rc;
         if ((rc = residual_launch(m, ly.o, IN_ATTN, st, li, position))) return rc;
     } else {
         if ((rc = qkv_launch(m, ly, li, position, st))) return rc;
@@ -633,10 +645,12 @@ extern "C" int fg_qwen2_step(fg_qwen2 *m, int token, size_t position, float *hid
     if (position >= sh.capacity) return set_error(FG_ERR_SHAPE, "fg_qwen2_step: the cache holds every key the span sees");
     if (token < 0 || size_t(token) >= sh.vocab) return set_error(FG_ERR_SHAPE, "fg_qwen2_step: token out of the vocabulary");
     hipStream_t st = as_stream(stream);
-    int rc = launch_dequantize_row(m->table, size_t(token), m->hidden, st);  // lm.rs:99-107
-    if (rc) return rc;
+    // the embedding row (lm.rs:99-107): in parallel order the first layer's launch reads it
+    int rc = FG_OK;
+    const bool fast = fast_attention(m);
+    if (!fast && (rc = launch_dequantize_row(m->table, size_t(token), m->hidden, st))) return rc;
     for (size_t l = 0; l < sh.layers; l++)
-        if ((rc = run_layer(m, l, position, st))) return rc;
+        if ((rc = run_layer(m, l, position, st, l == 0 && fast ? token : -1))) return rc;
     if (hidden) FG_HIP(hipMemcpyAsync(hidden, m->hidden, sh.hidden * 4, hipMemcpyDeviceToDevice, st));
     if (logits || next_token) {
         if ((rc = head_launch(m, st))) return rc;

@@ -61,6 +61,29 @@ __device__ __forceinline__ void tile_of(int L, int X, int Y, int &tx, int &ty)
     tx = in / rows;
 }
 
+// Activation scales of a tile's rows, transposed to [block][row] in LDS: this thread's row
+// `srow` (row-major, whole float4s), float4s c = part, part + parts, ... of n4. Eight loads go
+// out before their writes, so a pass waits for memory once rather than once per float4.
+template <int ROWS>
+__device__ __forceinline__ void stage_scales(float *tile_scales, const float *srow, int n4, int part, int parts, int row_in_tile)
+{
+    for (int c0 = part; c0 < n4; c0 += 8 * parts) {
+        v4f v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const v4f *>(srow + 4 * min(c0 + u * parts, n4 - 1));
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = c0 + u * parts;
+            if (c < n4) {
+                tile_scales[(4 * c) * ROWS + row_in_tile] = v[u].x;
+                tile_scales[(4 * c + 1) * ROWS + row_in_tile] = v[u].y;
+                tile_scales[(4 * c + 2) * ROWS + row_in_tile] = v[u].z;
+                tile_scales[(4 * c + 3) * ROWS + row_in_tile] = v[u].w;
+            }
+        }
+    }
+}
+
 // One wave per workgroup and per 32 x 32·TN output tile (TN MFMAs per block): enough waves to
 // spread the exact rescale, four VALU operations per output per block and the product's bound,
 // over every SIMD. Operands stream straight from memory, kDepth blocks ahead of the block being
@@ -101,14 +124,7 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     if (LDS_SCALES) {
         // rows m0 .. m0 + 31 of as (rows past M re-read the last), transposed to [block][row]:
         // lane l reads four blocks of row l % 32 and writes them to four consecutive-row slots
-        const float *srow = p.as + size_t(min(m0 + i, p.M - 1)) * p.G;
-        for (int c = h; c < B / 4; c += 2) {
-            const v4f v = *reinterpret_cast<const v4f *>(srow + 4 * c);
-            tile_scales[(4 * c) * 32 + i] = v.x;
-            tile_scales[(4 * c + 1) * 32 + i] = v.y;
-            tile_scales[(4 * c + 2) * 32 + i] = v.z;
-            tile_scales[(4 * c + 3) * 32 + i] = v.w;
-        }
+        stage_scales<32>(tile_scales, p.as + size_t(min(m0 + i, p.M - 1)) * p.G, B / 4, h, 2, i);
         __syncthreads();
     }
 
@@ -218,6 +234,127 @@ __global__ __launch_bounds__(64) void gemm_kernel(GemmParams p)
     }
 }
 
+// Four waves per 32 x 32 output tile, for products with too few tiles to give every SIMD a wave
+// of the kernel above. The exact order fixes only the additions: the terms
+// fl(fl((float)D_g) · fl(ws · as)) of different groups are independent. Wave w takes groups
+// w, w + 4, w + 8, ... (its own operands, its own ring of loads), forms its group's 1024 terms
+// and writes them to LDS; after one barrier per round of four groups, wave q adds the round's
+// four terms in group order to its quarter of the tile's sums (rows 8q + 4·(l/32) + 0..3 of
+// the MFMA layout). Every sum sees the reference's additions in the reference's order; the
+// rescale's VALU work and the operand waits spread over four SIMDs. Terms live in two buffers
+// (round parity): a wave writes round r + 2 only after the barrier of round r + 1, which every
+// wave reaches after reading round r.
+constexpr int kSplitDepth = 4;  // rounds each wave's ring of operands runs ahead
+
+template <int FMT>
+__global__ __launch_bounds__(256) void gemm_split_kernel(GemmParams p)
+{
+    extern __shared__ __align__(16) float split_lds[];  // [B][32] scales, then [2][4][4][64] v4f terms
+    constexpr int QB = FMT == 8 ? 128 : 64;
+    const int B = p.B;
+    float *tile_scales = split_lds;
+    v4f *terms = reinterpret_cast<v4f *>(split_lds + B * 32);
+    const int tid = threadIdx.x, lane = tid & 63, i = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tx, ty;
+    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 31) / 32, (p.M + 31) / 32, tx, ty);
+    const int m0 = ty * 32, n0 = p.col_begin + tx * 32;
+    const int row = min(m0 + i, p.M - 1);
+    const int8_t *arow = p.q + size_t(row) * p.K + h * 16;
+    const int nc = min(n0 + i, p.col_end - 1);
+    const int8_t *wrow = p.codes + size_t(nc >> 2) * B * QB + (nc & 3) * (QB / 4) + (FMT == 8 ? h * 16 : 0);
+    const float *wsrow = p.wscales + size_t(nc >> 2) * p.G * 4 + (nc & 3);
+    {
+        // rows m0 .. m0 + 31 of as, transposed to [block][row] (rows past M re-read the last)
+        stage_scales<32>(tile_scales, p.as + size_t(row) * p.G, B / 4, tid >> 5, 8, i);
+    }
+    struct Op {
+        v4i a, w;
+        float ws;
+    };
+    // group g of this wave's ring (past the last block: a clamped re-read, never used)
+    auto fetch = [&](int g, Op &o) {
+        const int b = min(g, B - 1);
+        o.a = *reinterpret_cast<const v4i *>(arow + b * 32);
+        o.w = *reinterpret_cast<const v4i *>(wrow + size_t(b) * QB);
+        o.ws = wsrow[size_t(b) * 4];
+    };
+    Op ring[kSplitDepth];
+#pragma unroll
+    for (int k = 0; k < kSplitDepth; k++) {
+        fetch(4 * k + wave, ring[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // the scales
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // The product of round r + 1 (this wave's group 4(r + 1) + wave; B is a multiple of 4, the
+    // launch checks it) and its scales' reads are issued between the barrier of round r and
+    // round r's additions, so their latencies overlap. Past the last round: clamped re-reads,
+    // never used.
+    v16i d;
+    v4f sc[4];
+    auto issue = [&](int r, const Op &o) {
+        const int g = min(4 * r + wave, B - 1);
+        const v4f *ls = reinterpret_cast<const v4f *>(tile_scales + g * 32 + 4 * h);
+#pragma unroll
+        for (int q = 0; q < 4; q++) sc[q] = ls[2 * q];  // rows 8q + 4h .. + 3
+        v4i w = o.w;
+        if (FMT == 4) {
+            const int sh = h * 4;
+            w = v4i{nibbles_signed(w.x >> sh), nibbles_signed(w.y >> sh), nibbles_signed(w.z >> sh), nibbles_signed(w.w >> sh)};
+        }
+        const v16i zero = {0};
+        d = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, w, zero, 0, 0, 0);
+        asm volatile("" : "+v"(d));  // keeps the product here rather than sunk to its first use
+    };
+    // round r: its terms to LDS, `o` refilled with the group kSplitDepth rounds on, the barrier,
+    // then the round's four groups added in order to this wave's quarter of the outputs
+    auto round = [&](int r, Op &o, const Op &o_next) {
+        const float ws = o.ws;
+        v4f *buf = terms + (r & 1) * (4 * 4 * 64);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            buf[(wave * 4 + q) * 64 + lane] = v4f{float(d[4 * q]) * (ws * sc[q].x), float(d[4 * q + 1]) * (ws * sc[q].y),
+                                                  float(d[4 * q + 2]) * (ws * sc[q].z), float(d[4 * q + 3]) * (ws * sc[q].w)};
+        fetch(4 * (r + kSplitDepth) + wave, o);
+        __syncthreads();
+        const v4f t0 = buf[wave * 64 + lane], t1 = buf[(4 + wave) * 64 + lane], t2 = buf[(8 + wave) * 64 + lane],
+                  t3 = buf[(12 + wave) * 64 + lane];
+        issue(r + 1, o_next);
+        __builtin_amdgcn_sched_barrier(0);  // the product goes out before the additions wait
+        acc[0] = acc[0] + t0.x + t1.x + t2.x + t3.x;
+        acc[1] = acc[1] + t0.y + t1.y + t2.y + t3.y;
+        acc[2] = acc[2] + t0.z + t1.z + t2.z + t3.z;
+        acc[3] = acc[3] + t0.w + t1.w + t2.w + t3.w;
+    };
+    // whole batches of kSplitDepth rounds without a branch (the load counts the compiler waits
+    // on stay exact), then the last rounds
+    const int rounds = B / 4;
+    issue(0, ring[0]);
+    int r0 = 0;
+    for (; r0 + kSplitDepth <= rounds; r0 += kSplitDepth) {
+#pragma unroll
+        for (int k = 0; k < kSplitDepth; k++) {
+            round(r0 + k, ring[k], ring[(k + 1) % kSplitDepth]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kSplitDepth - 1; k++)
+        if (r0 + k < rounds) round(r0 + k, ring[k], ring[k + 1]);
+    const int n = n0 + i;
+    if (n >= p.col_end) return;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int r = m0 + 8 * wave + 4 * h + e;
+        if (r >= p.M) continue;
+        float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+        float y = acc[e];
+        if (p.bias && n < p.n_rows) y = y + p.bias[n];
+        *o = p.accumulate ? *o + y : y;
+    }
+}
+
 // At most 16 rows: v_mfma_i32_16x16x32_i8, one wave per 16 x 16 tile. Weights, their scales and
 // the activations run kDepthW blocks ahead in rings of registers (loads complete in order, so
 // the activations' ring is as deep as the weights'). Deeper rings measured slower: the 16
@@ -245,14 +382,7 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     const float *wsrow = p.wscales + size_t(nc >> 2) * p.G * 4 + (nc & 3);
     if (!DOTS) {
         // the rows' scales, transposed to [block][row] (rows past M re-read the last)
-        const float *srow = p.as + size_t(row) * p.G;
-        for (int c = s; c < B / 4; c += 4) {
-            const v4f v = *reinterpret_cast<const v4f *>(srow + 4 * c);
-            tile_scales[(4 * c) * 16 + i] = v.x;
-            tile_scales[(4 * c + 1) * 16 + i] = v.y;
-            tile_scales[(4 * c + 2) * 16 + i] = v.z;
-            tile_scales[(4 * c + 3) * 16 + i] = v.w;
-        }
+        stage_scales<16>(tile_scales, p.as + size_t(row) * p.G, B / 4, s, 4, i);
         __syncthreads();
     }
     long rw[kDepthW], ra[kDepthA];
@@ -350,8 +480,15 @@ int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
         FG_HIP(hipGetLastError());
         return FG_OK;
     }
-    const long wide_waves = long((ncols + 63) / 64) * ((p.M + 31) / 32);
     const size_t smem = size_t(p.B) * 32 * 4;
+    // too few 32 x 32 tiles for two waves per SIMD: four waves per tile
+    const size_t split_smem = smem + 2 * 4 * 4 * 64 * 16;
+    if (!dots && lds && !FUSED && p.B % 4 == 0 && narrow_waves < 2048 && split_smem <= 64 * 1024) {
+        gemm_split_kernel<FMT><<<dim3{unsigned(narrow_waves)}, 256, split_smem, s>>>(p);
+        FG_HIP(hipGetLastError());
+        return FG_OK;
+    }
+    const long wide_waves = long((ncols + 63) / 64) * ((p.M + 31) / 32);
     if (wide_waves >= 1024) {
         const dim3 grid{unsigned(wide_waves)};
         if (dots) gemm_kernel<FMT, 2, true, false, false><<<grid, 64, 0, s>>>(p);

@@ -265,7 +265,7 @@ def test_prequantized_input_equals_in_kernel_quantization(fk, dtype, rows):
 
 
 @pytest.mark.parametrize("dtype", PRODUCT_FORMATS)
-@pytest.mark.parametrize("rows", [1, 6])
+@pytest.mark.parametrize("rows", [1, 6, 40])
 def test_column_ranges_bias_and_residual(fk, dtype, rows):
     import torch
     n_rows, cols = 50, 128

@@ -458,6 +458,90 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     }
 }
 
+// At most 16 rows with too few 16 x 16 tiles for two waves per SIMD: four waves per tile, split
+// over the groups as in gemm_split_kernel. Wave w forms the 256 terms of groups w, w + 4, ...
+// (four per lane: rows 4·(l/16) + v of column l % 16), writes them to LDS, and after the round's
+// barrier adds the round's four groups in order for output v = w of every lane.
+template <int FMT>
+__global__ __launch_bounds__(256) void gemm16_split_kernel(GemmParams p)
+{
+    extern __shared__ __align__(16) float split16_lds[];  // [B][16] scales, then [2][4][64] v4f terms
+    constexpr int QB = FMT == 8 ? 128 : 64;
+    const int B = p.B;
+    float *tile_scales = split16_lds;
+    v4f *terms = reinterpret_cast<v4f *>(split16_lds + B * 16);
+    const int tid = threadIdx.x, lane = tid & 63, i = lane & 15, sl = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tx, ty;
+    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 15) / 16, (p.M + 15) / 16, tx, ty);
+    const int m0 = ty * 16, n0 = p.col_begin + tx * 16;
+    const int row = min(m0 + i, p.M - 1);
+    const int n = n0 + i, nc = min(n, p.col_end - 1);
+    const int8_t *arow = p.q + size_t(row) * p.K + 8 * sl;
+    const int8_t *wrow = p.codes + size_t(nc >> 2) * B * QB + (nc & 3) * (QB / 4) + (FMT == 8 ? 8 * sl : 8 * (sl & 1));
+    const int shift = FMT == 8 ? 0 : 4 * (sl >> 1);
+    const float *wsrow = p.wscales + size_t(nc >> 2) * p.G * 4 + (nc & 3);
+    stage_scales<16>(tile_scales, p.as + size_t(row) * p.G, B / 4, tid >> 4, 16, i);
+    struct Op {
+        long a, w;
+        float ws;
+    };
+    auto fetch = [&](int g, Op &o) {
+        const int b = min(g, B - 1);
+        o.a = *reinterpret_cast<const long *>(arow + b * 32);
+        o.w = *reinterpret_cast<const long *>(wrow + size_t(b) * QB);
+        o.ws = wsrow[size_t(b) * 4];
+    };
+    Op ring[kSplitDepth];
+#pragma unroll
+    for (int k = 0; k < kSplitDepth; k++) {
+        fetch(4 * k + wave, ring[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // the scales
+    float acc = 0.0f;
+    // round r (B is a multiple of 4: the launch checks it)
+    auto round = [&](int r, Op &o) {
+        const int g = 4 * r + wave;
+        const v4f sc = *reinterpret_cast<const v4f *>(tile_scales + g * 16 + 4 * sl);
+        long w = o.w;
+        if (FMT == 4) {
+            const int lo = nibbles_signed(int(w) >> shift), hi = nibbles_signed(int(w >> 32) >> shift);
+            w = long(unsigned(lo)) | (long(hi) << 32);
+        }
+        const v4i zero = {0, 0, 0, 0};
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a, w, zero, 0, 0, 0);
+        const float ws = o.ws;
+        v4f *buf = terms + (r & 1) * (4 * 64);
+        buf[wave * 64 + lane] = v4f{float(d[0]) * (ws * sc.x), float(d[1]) * (ws * sc.y), float(d[2]) * (ws * sc.z),
+                                    float(d[3]) * (ws * sc.w)};
+        fetch(4 * (r + kSplitDepth) + wave, o);
+        __syncthreads();
+        const float *fb = reinterpret_cast<const float *>(buf);
+        const float t0 = fb[(0 * 64 + lane) * 4 + wave], t1 = fb[(1 * 64 + lane) * 4 + wave],
+                    t2 = fb[(2 * 64 + lane) * 4 + wave], t3 = fb[(3 * 64 + lane) * 4 + wave];
+        acc = acc + t0 + t1 + t2 + t3;
+    };
+    const int rounds = B / 4;
+    int r0 = 0;
+    for (; r0 + kSplitDepth <= rounds; r0 += kSplitDepth) {
+#pragma unroll
+        for (int k = 0; k < kSplitDepth; k++) {
+            round(r0 + k, ring[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kSplitDepth - 1; k++)
+        if (r0 + k < rounds) round(r0 + k, ring[k]);
+    const int r = m0 + 4 * sl + wave;
+    if (n >= p.col_end || r >= p.M) return;
+    float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+    float y = acc;
+    if (p.bias && n < p.n_rows) y = y + p.bias[n];
+    *o = p.accumulate ? *o + y : y;
+}
+
 // as [M][G] -> as_t [G][Mpad] (zeros past M).
 __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int G, int Mpad, float *__restrict__ as_t)
 {
@@ -475,6 +559,14 @@ int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
     const long narrow_waves = long((ncols + 31) / 32) * ((p.M + 31) / 32);
     if (p.M <= 16 && (dots || lds)) {
         const dim3 grid(unsigned(((ncols + 15) / 16) * ((p.M + 15) / 16)));
+        // fewer than 512 tiles: four waves per tile (16 x 4864 -> 896: 18.5 -> 11.6 us; at 896
+        // tiles, 16 x 4096 -> 14336 Q4, one wave per tile is faster: 27.8 against 31.5 us)
+        const size_t split16_smem = size_t(p.B) * 16 * 4 + 2 * 4 * 64 * 16;
+        if (!dots && !FUSED && p.B % 4 == 0 && grid.x < 512 && split16_smem <= 64 * 1024) {
+            gemm16_split_kernel<FMT><<<grid, 256, split16_smem, s>>>(p);
+            FG_HIP(hipGetLastError());
+            return FG_OK;
+        }
         if (dots) gemm16_kernel<FMT, true, false><<<grid, 64, 0, s>>>(p);
         else gemm16_kernel<FMT, false, FUSED><<<grid, 64, size_t(p.B) * 16 * 4, s>>>(p);
         FG_HIP(hipGetLastError());

@@ -369,6 +369,21 @@ def test_int4_shape_bit_exact(fk, rows):
     assert same_bits(got[sample], want), first_mismatch(got[sample], want)
 
 
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+@pytest.mark.parametrize("rows", [16, 40])
+def test_split_rounds_with_whole_batches_and_a_tail(fk, dtype, rows):
+    """Few tiles, long rows: four waves per tile take turns over the groups (11 rounds of four
+    groups: two whole batches of four rounds and a tail of three), every sum in group order."""
+    n, k = 96, 32 * 44
+    data = synthetic_table(dtype, n, k, seed=rows + 7)
+    t = table(fk, dtype, n, k, data)
+    x = activations(rows, k, seed=rows + 70, outliers=0.02)
+    bias = np.random.default_rng(4).standard_normal(n).astype(np.float32)
+    got = gpu_product(fk, t, x, rows, bias=bias)
+    want = oracle_product(dtype, n, k, data, x, rows, bias=bias)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
 @pytest.mark.parametrize("rows", [5, 11, 16])
 def test_small_batch_over_whole_tiles_bit_exact(fk, dtype, rows):

@@ -3,11 +3,12 @@
 The names follow the reference crate's public API (kernels/src/lib.rs:22-31): DType, Tensor,
 Table, Matrix, Vector, QuantFormat, QuantizedRows, Quantized, Input, quantize_rows, matmul,
 Linear, project, project_input, project_residual, project_residual_input, conv.project_rows,
-QuantizedMatrix and the constants. Every computation runs in the
+QuantizedMatrix and the constants, and the blocks crate's int8 attention (attention::attend). Every computation runs in the
 HIP library libfusor_gpu.so through its C ABI (include/fusor_gpu.h); there is no CPU fallback.
 """
 
 from ._lib import Error, FormatError, GpuError, ShapeError, lib
+from .attention import Call, Exponentials, Operand, attend
 from .conv import Patches, project_rows
 from .linear import (COLUMN_ALIGN, NARROW_COLUMN_ALIGN, Ctx, Linear, SharedRows, project, project_input,
                      project_residual, project_residual_input)
@@ -21,6 +22,6 @@ __all__ = [
     "DType", "QuantFormat", "Tensor", "Table", "Matrix", "Vector", "byte_len",
     "QuantizedRows", "QuantizedMatrix", "Quantized", "Input", "quantize_rows", "matmul", "matmul_dots",
     "Linear", "Ctx", "SharedRows", "project", "project_input", "project_residual", "project_residual_input",
-    "Patches", "project_rows", "Qwen2", "Shape",
+    "Patches", "project_rows", "Qwen2", "Shape", "Call", "Operand", "Exponentials", "attend",
     "Error", "FormatError", "ShapeError", "GpuError", "lib",
 ]

@@ -24,6 +24,13 @@ class FgInput(ctypes.Structure):
     _fields_ = [("x", _P), ("quants", _P), ("scales", _P), ("corrections", _P)]
 
 
+class FgAttention(ctypes.Structure):
+    _fields_ = [("heads", _S), ("kv_heads", _S), ("head_dim", _S), ("images", _S), ("queries", _S), ("keys", _S),
+                ("query", _P), ("query_stride", _S), ("query_offset", _S),
+                ("key", _P), ("key_stride", _S), ("key_offset", _S),
+                ("value", _P), ("value_stride", _S), ("value_offset", _S), ("exponentials", _I)]
+
+
 class FgQwen2Shape(ctypes.Structure):
     _fields_ = [("hidden", _S), ("layers", _S), ("heads", _S), ("kv_heads", _S), ("head_dim", _S),
                 ("ffn", _S), ("vocab", _S), ("capacity", _S), ("rope_base", _F), ("eps", _F),
@@ -52,6 +59,7 @@ SIGNATURES = {
     "fg_qmatrix_extend": (_I, [_P, _S, _P]),
     "fg_qmatrix_set_rows": (_I, [_P, _S, _S, _P, _P]),
     "fg_qmatrix_set_block": (_I, [_P, _S, _S, _P, _P]),
+    "fg_attend": (_I, [ctypes.POINTER(FgAttention), _P, _P]),
     "fg_quantize_rows": (_I, [_P, _S, _I, _P, _P, _P, _P]),
     "fg_matmul": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P, _S, _I, _P]),
     "fg_matmul_dots": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P]),

@@ -103,6 +103,33 @@ int fg_qmatrix_set_rows(fg_table *matrix, size_t row, size_t count, const float 
 /* QuantizedMatrix::set_block (matmul.rs:77-90): block `block` of row `row` from 32 device f32. */
 int fg_qmatrix_set_block(fg_table *matrix, size_t row, size_t block, const float *values, void *stream);
 
+/* ------------------------------------------------------------------- int8 attention */
+
+/* Exponentials (ops.rs:163-166): `exp` (within 2 ulp) or `exp_fast` (within 6e-5, fused). */
+#define FG_EXP_EXACT 0
+#define FG_EXP_FAST 1
+
+/* attention::Call (blocks/src/attention.rs:35-47) with its three Operands (:24-30): head h of
+ * row r of an operand is the head_dim device f32 values at r * stride + offset + h * head_dim.
+ * `images` images of `queries` query rows over `keys` key and value rows; `heads` query heads
+ * share `kv_heads` key heads in consecutive runs. */
+typedef struct fg_attention {
+    size_t heads, kv_heads, head_dim, images, queries, keys;
+    const float *query;
+    size_t query_stride, query_offset;
+    const float *key;
+    size_t key_stride, key_offset;
+    const float *value;
+    size_t value_stride, value_offset;
+    int exponentials; /* FG_EXP_EXACT or FG_EXP_FAST */
+} fg_attention;
+
+/* attention::attend (blocks/src/attention.rs:81-214) for the whole call, into device `out`
+ * [images * queries][heads * head_dim]: keys and values quantized at run time (Q7b32 rows),
+ * both products on the quantized kernels, the reference's f32 order around them. head_dim whole
+ * quads, at most 16384 keys. Returns once the work on `stream` has finished. */
+int fg_attend(const fg_attention *call, float *out, void *stream);
+
 /* ------------------------------------------------------------------------ activations */
 
 /* quantize_rows (matmul.rs:233-257): `count` device f32 values, whole groups of the weight

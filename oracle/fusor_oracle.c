@@ -494,6 +494,46 @@ float or_exp(float x)
 
 float or_silu(float x) { return x / (1.0f + or_exp(-x)); }
 
+/* ops.rs:137-153: x clamped below at EXP_MIN, n = round(x·log2 e) (ties to even), r = fma(-n,
+ * ln 2, x), the degree-4 Taylor polynomial in fused multiply-adds (Rust's mul_add, the scalar
+ * backend's arithmetic), times 2^n. */
+float or_exp_fast(float x)
+{
+    static const float taylor[5] = {1.0f / 24.0f, 1.0f / 6.0f, 0.5f, 1.0f, 1.0f};
+    const float log2_e = 1.44269504088896340736f, ln_2 = 0.693147180559945309417f;
+    x = fmaxf(x, -87.0f);
+    float exponent = rintf(x * log2_e);
+    float remainder = fmaf(-exponent, ln_2, x);
+    float poly = taylor[0];
+    for (int i = 1; i < 5; i++) poly = fmaf(poly, remainder, taylor[i]);
+    uint32_t bits = (uint32_t)((sat_i32(exponent) + 127) << 23);
+    float two_n;
+    memcpy(&two_n, &bits, sizeof two_n);
+    return poly * two_n;
+}
+
+/* Exponentials::apply (ops.rs:168-191) on the scalar backend: the maximum as a fold from -inf
+ * (scalar.rs:52-55); the sweep over whole runs of EXP_RUN = 8 values (arch/mod.rs:46), each
+ * value's exponential added to the sum of its offset in the run (scalar.rs:117-126); the rest
+ * one by one; then the rest's values and the eight offset sums added in that order. */
+float or_exponentials_apply(float *scores, size_t n, int fast)
+{
+    float max = -INFINITY;
+    for (size_t i = 0; i < n; i++) max = fmaxf(max, scores[i]);
+    float sums[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const size_t whole = n / 8 * 8;
+    for (size_t i = 0; i < whole; i++) {
+        const float v = fast ? or_exp_fast(scores[i] - max) : or_exp(scores[i] - max);
+        scores[i] = v;
+        sums[i % 8] = sums[i % 8] + v;
+    }
+    for (size_t i = whole; i < n; i++) scores[i] = fast ? or_exp_fast(scores[i] - max) : or_exp(scores[i] - max);
+    float total = -0.0f;
+    for (size_t i = whole; i < n; i++) total = total + scores[i];
+    for (int k = 0; k < 8; k++) total = total + sums[k];
+    return total;
+}
+
 /* scalar.rs:340-342: a float sum in index order from -0.0 */
 float or_dot_f32(const float *a, const float *b, size_t n)
 {
@@ -546,6 +586,91 @@ void or_softmax(float *scores, size_t n)
     float total = -0.0f;
     for (size_t i = 0; i < n; i++) total = total + scores[i];
     for (size_t i = 0; i < n; i++) scores[i] = scores[i] / total;
+}
+
+/* ------------------------------------------------- int8 attention (blocks/src/attention.rs) */
+
+static size_t pad32(size_t n) { return (n + 31) / 32 * 32; }
+
+/* attention::attend (attention.rs:81-95) over every (image, head, block of queries); each unit
+ * (attention.rs:157-214) is independent, so the units' order does not change a bit. Per (image,
+ * key head) (Scratch::quantize, attention.rs:100-137): the keys' mean over the keys in order,
+ * divided by their count; each key less the mean, zero-padded to whole blocks, pushed as a
+ * Q7b32 row; the values transposed, one Q7b32 row per channel over the keys padded with zeros.
+ * Per unit: the queries zero-padded and quantized; scores = the keys' product over the keys
+ * rounded up to a quad, each times 1/sqrt(head_dim), zeros past them; Exponentials::apply over
+ * the first `keys`; the scores' rows quantized (their whole padded width); the values' product
+ * over the channels, each divided by its row's sum. Returns -1 on a shape error. */
+int or_attend(const or_attention *c, float *out)
+{
+    const size_t hd = c->head_dim, keys = c->keys, queries = c->queries;
+    if (!hd || !keys || !queries || !c->heads || !c->kv_heads || c->heads % c->kv_heads || hd % 4) return -1;
+    const size_t pd = pad32(hd), pk = pad32(keys), keys4 = (keys + 3) / 4 * 4;
+    const size_t stride = c->heads * hd, group = c->heads / c->kv_heads;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *mean = malloc(hd * sizeof(float));
+    float *krows = malloc(keys * pd * sizeof(float)), *vrows = malloc(hd * pk * sizeof(float));
+    uint8_t *kbytes = malloc(or_byte_len(OR_Q7B32, keys, pd)), *vbytes = malloc(or_byte_len(OR_Q7B32, hd, pk));
+    float *qrows = malloc(32 * pd * sizeof(float)), *scores = malloc(32 * pk * sizeof(float));
+    float *prod = malloc(32 * (keys4 > hd ? keys4 : hd) * sizeof(float)), sums[32];
+    const size_t wide = pd > pk ? pd : pk;
+    int8_t *q = malloc(32 * wide);
+    float *qs = malloc(32 * (wide / 32) * sizeof(float));
+    int32_t *qc = malloc(32 * (wide / 32) * sizeof(int32_t));
+    int rc = 0;
+    for (size_t image = 0; image < c->images && !rc; image++) {
+        for (size_t kh = 0; kh < c->kv_heads && !rc; kh++) {
+            const size_t first = image * keys;
+            for (size_t d = 0; d < hd; d++) mean[d] = 0.0f;
+            for (size_t k = 0; k < keys; k++) {
+                const float *row = c->key + (first + k) * c->key_stride + c->key_offset + kh * hd;
+                for (size_t d = 0; d < hd; d++) mean[d] = mean[d] + row[d];
+            }
+            for (size_t d = 0; d < hd; d++) mean[d] = mean[d] / (float)keys;
+            for (size_t k = 0; k < keys; k++) {
+                const float *row = c->key + (first + k) * c->key_stride + c->key_offset + kh * hd;
+                for (size_t d = 0; d < pd; d++) krows[k * pd + d] = d < hd ? row[d] - mean[d] : 0.0f;
+            }
+            for (size_t d = 0; d < hd; d++)
+                for (size_t k = 0; k < pk; k++)
+                    vrows[d * pk + k] = k < keys ? c->value[(first + k) * c->value_stride + c->value_offset + kh * hd + d] : 0.0f;
+            /* encoding packs codes into zeroed quads; padding rows keep zero codes and scales */
+            memset(kbytes, 0, or_byte_len(OR_Q7B32, keys, pd));
+            memset(vbytes, 0, or_byte_len(OR_Q7B32, hd, pk));
+            if (or_encode(OR_Q7B32, keys, pd, krows, kbytes) || or_encode(OR_Q7B32, hd, pk, vrows, vbytes)) {
+                rc = -1;
+                break;
+            }
+            for (size_t h = kh * group; h < (kh + 1) * group && !rc; h++) {
+                for (size_t q0 = 0; q0 < queries; q0 += 32) {
+                    const size_t nq = queries - q0 < 32 ? queries - q0 : 32, qfirst = image * queries + q0;
+                    for (size_t r = 0; r < nq; r++) {
+                        const float *row = c->query + (qfirst + r) * c->query_stride + c->query_offset + h * hd;
+                        for (size_t d = 0; d < pd; d++) qrows[r * pd + d] = d < hd ? row[d] : 0.0f;
+                    }
+                    or_quantize_rows(qrows, nq * pd, OR_Q7B32, q, qs, qc);
+                    if (or_matmul(OR_Q7B32, keys, pd, kbytes, q, qs, qc, nq, 0, keys4, NULL, prod, keys4, NULL)) {
+                        rc = -1;
+                        break;
+                    }
+                    for (size_t r = 0; r < nq; r++) {
+                        for (size_t k = 0; k < pk; k++) scores[r * pk + k] = k < keys4 ? prod[r * keys4 + k] * scale : 0.0f;
+                        sums[r] = or_exponentials_apply(scores + r * pk, keys, c->fast);
+                    }
+                    or_quantize_rows(scores, nq * pk, OR_Q7B32, q, qs, qc);
+                    if (or_matmul(OR_Q7B32, hd, pk, vbytes, q, qs, qc, nq, 0, hd, NULL, prod, hd, NULL)) {
+                        rc = -1;
+                        break;
+                    }
+                    for (size_t r = 0; r < nq; r++)
+                        for (size_t d = 0; d < hd; d++) out[(qfirst + r) * stride + h * hd + d] = prod[r * hd + d] / sums[r];
+                }
+            }
+        }
+    }
+    free(mean); free(krows); free(vrows); free(kbytes); free(vbytes); free(qrows); free(scores); free(prod);
+    free(q); free(qs); free(qc);
+    return rc;
 }
 
 /* ---------------------------------------------------------------------- rng (rng.rs) */

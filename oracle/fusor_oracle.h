@@ -111,6 +111,10 @@ int or_matmul_threaded(int dtype, size_t n_rows, size_t cols, const uint8_t *byt
 /* f32 operations (ops.rs). */
 float or_exp(float x);                                   /* ops.rs:121-131 */
 float or_silu(float x);                                  /* ops.rs:272-274 */
+float or_exp_fast(float x);                              /* ops.rs:137-153 */
+/* Exponentials::apply (ops.rs:168-191), scalar backend: scores replaced by their exponentials
+ * less the maximum (fast: exp_fast, else exp); returns their sum in the backend's order. */
+float or_exponentials_apply(float *scores, size_t n, int fast);
 float or_dot_f32(const float *a, const float *b, size_t n); /* scalar.rs:340-342 */
 void or_rms_norm(const float *x, const float *weight, size_t dim, float eps, float *out);
 void or_rope_inv_freq(float base, size_t head_dim, float *inv_freq);     /* ops.rs:70-74 */
@@ -154,6 +158,22 @@ int or_qwen2_step(const or_qwen2_shape *shape, const or_qwen2_layer *layers,
                   int token, size_t position, float *hidden_out, float *logits, int *next_token,
                   int threads);
 int or_greedy(const float *logits, size_t n); /* lm.rs:169-179 */
+
+/* One int8 attention call (blocks/src/attention.rs:35-47): head h of row r of an operand is the
+ * head_dim values at r * stride + offset + h * head_dim; `images` images of `queries` query rows
+ * over `keys` key and value rows; query heads share key heads in consecutive runs. */
+typedef struct {
+    size_t heads, kv_heads, head_dim, images, queries, keys;
+    const float *query;
+    size_t query_stride, query_offset;
+    const float *key;
+    size_t key_stride, key_offset;
+    const float *value;
+    size_t value_stride, value_offset;
+    int fast; /* Exponentials::Fast, else Exact */
+} or_attention;
+/* attention::attend (attention.rs:81-214) into out [images * queries][heads * head_dim]. */
+int or_attend(const or_attention *call, float *out);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,14 @@ class Qwen2Layer(ctypes.Structure):
                 ("up", _P), ("down", _P), ("qkv_bias", _P)]
 
 
+class Attention(ctypes.Structure):
+    """or_attention: one int8 attention call (blocks/src/attention.rs:35-47)."""
+    _fields_ = [("heads", _S), ("kv_heads", _S), ("head_dim", _S), ("images", _S), ("queries", _S), ("keys", _S),
+                ("query", _P), ("query_stride", _S), ("query_offset", _S),
+                ("key", _P), ("key_stride", _S), ("key_offset", _S),
+                ("value", _P), ("value_stride", _S), ("value_offset", _S), ("fast", _I)]
+
+
 def _declare(l):
     sig = {
         "or_group": (_I, [_I]), "or_zero_point": (_I, [_I]), "or_codes_per_byte": (_I, [_I]),
@@ -69,6 +77,8 @@ def _declare(l):
         "or_matmul_fused": (_I, [_I, _S, _S, _P, _P, _P, _P, _S, _S, _S, _P, _P, _S, _P, _I]),
         "or_matmul_threaded": (_I, [_I, _S, _S, _P, _P, _P, _P, _S, _P, _P, _I]),
         "or_exp": (_F, [_F]), "or_silu": (_F, [_F]),
+        "or_exp_fast": (_F, [_F]), "or_exponentials_apply": (_F, [_P, _S, _I]),
+        "or_attend": (_I, [_P, _P]),
         "or_dot_f32": (_F, [_P, _P, _S]),
         "or_rms_norm": (None, [_P, _P, _S, _F, _P]),
         "or_rope_inv_freq": (None, [_F, _S, _P]),
@@ -194,6 +204,36 @@ def matmul_threaded(dtype, n_rows, cols, table, q, s, c, rows, bias=None, thread
 
 def exp(x):
     return np.float32(lib().or_exp(float(np.float32(x))))
+
+
+def exp_fast(x):
+    return np.float32(lib().or_exp_fast(float(np.float32(x))))
+
+
+def exponentials_apply(scores, fast):
+    """Exponentials::apply (ops.rs:168-191): (the exponentials, their sum)."""
+    v = np.ascontiguousarray(scores, dtype=np.float32).copy()
+    total = lib().or_exponentials_apply(_ptr(v), v.size, int(bool(fast)))
+    return v, np.float32(total)
+
+
+def attend(heads, kv_heads, head_dim, images, queries, keys, query, key, value, fast=False,
+           query_layout=None, key_layout=None, value_layout=None):
+    """attention::attend (blocks/src/attention.rs:81-214). Operands are flat f32 arrays with a
+    (stride, offset) layout each (default: rows of heads * head_dim, or kv_heads * head_dim);
+    returns [images * queries, heads * head_dim]."""
+    q = np.ascontiguousarray(query, dtype=np.float32).reshape(-1)
+    k = np.ascontiguousarray(key, dtype=np.float32).reshape(-1)
+    v = np.ascontiguousarray(value, dtype=np.float32).reshape(-1)
+    ql = query_layout or (heads * head_dim, 0)
+    kl = key_layout or (kv_heads * head_dim, 0)
+    vl = value_layout or (kv_heads * head_dim, 0)
+    out = np.zeros((images * queries, heads * head_dim), dtype=np.float32)
+    call = Attention(heads, kv_heads, head_dim, images, queries, keys, _ptr(q), ql[0], ql[1], _ptr(k), kl[0], kl[1],
+                     _ptr(v), vl[0], vl[1], int(bool(fast)))
+    if lib().or_attend(ctypes.byref(call), _ptr(out)):
+        raise ValueError("attend: shapes do not fit")
+    return out
 
 
 def silu(x):

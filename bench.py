@@ -324,6 +324,20 @@ def extras(fk, torch, np):
         ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 50, graph=True)
         b = n * k // 2 + n * k // 32 * 4 + rows * (k + k // 32 * 8) + rows * n * 4
         res[f"int4_14336x4096_rows{rows}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
+    # 4. int8 attention (attention::attend) at the DiT block's shape: 4096 tokens, 16 heads of 72
+    #    read by stride and offset from one fused qkv row, exp_fast; each call quantizes the keys
+    #    and values, allocates its scratch and waits for its stream
+    tokens, heads, hd = 4096, 16, 72
+    row = 3 * heads * hd
+    qkv = torch.from_numpy(rng.standard_normal((tokens, row)).astype(np.float32)).cuda()
+    out = torch.empty((tokens, heads * hd), dtype=torch.float32, device="cuda")
+    call = fk.Call(heads, heads, hd, 1, tokens, tokens, fk.Operand(qkv, row, 0), fk.Operand(qkv, row, heads * hd),
+                   fk.Operand(qkv, row, 2 * heads * hd), fk.Exponentials.FAST)
+    ms = timer(lambda: fk.attend(call, out), 3, warmup=1)
+    padded_hd = (hd + 31) // 32 * 32
+    ops = 2.0 * heads * tokens * tokens * (padded_hd + hd)  # Q·K over the padded head, P·V
+    res["int8_attention_dit_4096x16x72"] = {"ms": round(ms, 3), "int8_TOPS": round(ops / ms / 1e9, 1)}
+    del qkv, out
     return res
 
 

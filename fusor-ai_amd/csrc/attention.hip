@@ -43,15 +43,29 @@ __device__ __forceinline__ float ref_exp_fast(float x)
     return poly * __int_as_float((int(n) + 127) << 23);
 }
 
-// mean[d] = (Σ over the keys in order of key[d]) / keys, one thread per channel
-__global__ void key_mean_kernel(const float *__restrict__ key, size_t stride, size_t base, int keys, int hd,
-                                float *__restrict__ mean)
+// mean[(image · kv_heads + kh) · hd + d] = (Σ over the image's keys in order of key[d]) / keys,
+// one thread per (image, key head, channel), every key head of the call in one launch; each
+// thread issues 32 keys' loads before it adds them, in order
+__global__ void key_mean_kernel(const float *__restrict__ key, size_t stride, size_t offset, int images, int kv_heads,
+                                int keys, int hd, float *__restrict__ mean)
 {
-    const int d = blockIdx.x * blockDim.x + threadIdx.x;
-    if (d >= hd) return;
+    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= size_t(images) * kv_heads * hd) return;
+    const int d = int(i % hd);
+    const size_t ih = i / hd;
+    const int kh = int(ih % kv_heads);
+    const size_t image = ih / kv_heads;
+    const float *base = key + image * size_t(keys) * stride + offset + size_t(kh) * hd + d;
     float s = 0.0f;
-    for (int k = 0; k < keys; k++) s = s + key[base + size_t(k) * stride + d];
-    mean[d] = s / float(keys);
+    for (int k0 = 0; k0 < keys; k0 += 32) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; u++) v[u] = base[size_t(min(k0 + u, keys - 1)) * stride];
+#pragma unroll
+        for (int u = 0; u < 32; u++)
+            if (k0 + u < keys) s = s + v[u];
+    }
+    mean[i] = s / float(keys);
 }
 
 // rows[k][d] = key[k][d] − mean[d] for d < hd, zeros to the padded width pd
@@ -107,8 +121,18 @@ __global__ __launch_bounds__(64) void exponentials_kernel(const float *__restric
     __syncthreads();
     const int whole = keys / 8 * 8;
     float part = 0.0f;
-    if (lane < 8)
-        for (int i = lane; i < whole; i += 8) part = part + row[i];
+    if (lane < 8) {
+        // sixteen reads out before their sixteen additions, in run order
+        int i = lane;
+        for (; i + 8 * 15 < whole; i += 8 * 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = row[i + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) part = part + v[u];
+        }
+        for (; i < whole; i += 8) part = part + row[i];
+    }
     float total = -0.0f;
     if (lane == 0) {
         for (int i = whole; i < keys; i++) total = total + row[i];
@@ -146,7 +170,7 @@ int run(const fg_attention *c, float *out, hipStream_t st, Scratch &w)
     const int pd = int(pad32(c->head_dim)), pk = int(pad32(c->keys)), keys4 = (keys + 3) / 4 * 4;
     const size_t group = c->heads / c->kv_heads, stride = c->heads * c->head_dim;
     const float scale = 1.0f / sqrtf(float(hd));
-    const size_t bytes[] = {size_t(hd) * 4,  size_t(keys) * pd * 4,
+    const size_t bytes[] = {c->images * c->kv_heads * size_t(hd) * 4, size_t(keys) * pd * 4,
                             size_t(hd) * pk * 4, size_t(queries) * pd * 4,
                             size_t(queries) * size_t(keys4 > hd ? keys4 : hd) * 4,
                             size_t(queries) * pk * 4, size_t(queries) * 4};
@@ -155,14 +179,16 @@ int run(const fg_attention *c, float *out, hipStream_t st, Scratch &w)
     int rc;
     if ((rc = fg_qmatrix_create(size_t(keys), size_t(pd), &w.keys)) || (rc = fg_qmatrix_create(size_t(hd), size_t(pk), &w.values)))
         return rc;
+    key_mean_kernel<<<blocks_for(c->images * c->kv_heads * size_t(hd)), kThreads, 0, st>>>(
+        c->key, c->key_stride, c->key_offset, int(c->images), int(c->kv_heads), keys, hd, w.mean);
+    FG_HIP(hipGetLastError());
     for (size_t image = 0; image < c->images; image++) {
         for (size_t kh = 0; kh < c->kv_heads; kh++) {
             // Scratch::quantize (attention.rs:100-137)
             const size_t kbase = image * c->keys * c->key_stride + c->key_offset + kh * c->head_dim;
             const size_t vbase = image * c->keys * c->value_stride + c->value_offset + kh * c->head_dim;
-            key_mean_kernel<<<blocks_for(hd), kThreads, 0, st>>>(c->key, c->key_stride, kbase, keys, hd, w.mean);
-            key_rows_kernel<<<blocks_for(size_t(keys) * pd), kThreads, 0, st>>>(c->key, c->key_stride, kbase, keys, hd, pd,
-                                                                                w.mean, w.krows);
+            key_rows_kernel<<<blocks_for(size_t(keys) * pd), kThreads, 0, st>>>(
+                c->key, c->key_stride, kbase, keys, hd, pd, w.mean + (image * c->kv_heads + kh) * size_t(hd), w.krows);
             value_rows_kernel<<<blocks_for(size_t(hd) * pk), kThreads, 0, st>>>(c->value, c->value_stride, vbase, keys, hd,
                                                                                 pk, w.vrows);
             FG_HIP(hipGetLastError());

@@ -8,8 +8,8 @@
  * Every function restates the x86-64 ("scalar backend") semantics of the Rust reference; the
  * file:line citations are relative to the fusor-ai checkout (crates/kernels/src unless noted).
  * Arithmetic rules it keeps: IEEE f32 division and sqrt, ties-to-even rounding, no fused
- * multiply-add anywhere (built with -ffp-contract=off), saturating float->int casts, float sums
- * in index order from -0.0.
+ * multiply-add anywhere (built with -ffp-contract=off) except where the reference calls mul_add
+ * (exp_fast), saturating float->int casts, float sums in index order from -0.0.
  *
  * What pins each part (tests/test_oracle.py, tests/test_golden.py); the reference is Rust and
  * cannot be built or run here, so nothing is pinned by running it:
@@ -23,6 +23,13 @@
  *     sequential, unfused numpy evaluation and an FMA variant that must differ; the reference
  *     test's own f64 tolerance 1e-4 (1 + |want|) on its own inputs (matmul.rs:809-843);
  *   exp, silu, rms_norm, softmax, rotary angles: closed forms and f64 within stated bounds;
+ *   exp_fast, exponentials_apply (tests/test_oracle_attention.py): exp_fast within its stated
+ *     6e-5 (ops.rs:137-139) and unlike an unfused evaluation; equal scores summing to their
+ *     count exactly; the maximum's exponential 1; the sum against math.fsum of the values;
+ *   attend: an independent f64 attention within the Q7b32 stack tolerance over grouped heads,
+ *     images, padded sizes and fused operands, and invariance to a shift of every key (the
+ *     keys' mean). Its f32 order (the mean, the exponentials' sum) follows the cited code and is
+ *     parity unpinned at the bit level: the reference holds no attention fixture;
  *   rng: SplitMix64's published first output and xoshiro256**'s definition;
  *   qwen2 layer and step: an independent f64 evaluation of the same model within the
  *     reference's own tolerance for a Q7b32 stack (3e-2 relative L2, blocks/tests/stacks.rs:49-55).

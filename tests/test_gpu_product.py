@@ -370,6 +370,22 @@ def test_int4_shape_bit_exact(fk, rows):
 
 
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+@pytest.mark.parametrize("rows", [5, 16])
+def test_small_batch_with_staged_rows_over_many_columns(fk, dtype, rows):
+    """5-16 rows over 515 tiles of 16 columns (the last workgroup's columns partly past the
+    table): the activation rows staged in LDS in slabs of 64 blocks, a whole slab and a partial
+    one of 8."""
+    n, k = 8228, 32 * 72
+    data = synthetic_table(dtype, n, k, seed=rows + 17)
+    t = table(fk, dtype, n, k, data)
+    x = activations(rows, k, seed=rows + 71, outliers=0.02)
+    bias = np.random.default_rng(6).standard_normal(n).astype(np.float32)
+    got = gpu_product(fk, t, x, rows, bias=bias)
+    want = oracle_product(dtype, n, k, data, x, rows, bias=bias)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
 @pytest.mark.parametrize("rows", [16, 40])
 def test_split_rounds_with_whole_batches_and_a_tail(fk, dtype, rows):
     """Few tiles, long rows: four waves per tile take turns over the groups (11 rounds of four

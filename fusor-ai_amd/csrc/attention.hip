@@ -98,52 +98,59 @@ __global__ void query_rows_kernel(const float *__restrict__ query, size_t stride
     rows[i] = d < hd ? query[base + size_t(r) * stride + d] : 0.0f;
 }
 
-// One wave per query row: the row's scores (product · scale below keys4, zeros to pk) staged in
-// LDS, their maximum over the first `keys`, the exponentials there, and their sum in the scalar
-// backend's order (scalar.rs:117-126, ops.rs:170-175): lane o < 8 sums offset o over the whole
-// runs of eight in order, lane 0 adds the rest in order, then the eight offset sums in order.
+// One workgroup of four waves per query row: the row's scores (product · scale below keys4,
+// zeros to pk) staged in LDS, their maximum over the first `keys`, the exponentials there (all
+// 256 threads), and their sum in the scalar backend's order (scalar.rs:117-126, ops.rs:170-175):
+// lane o < 8 of the first wave sums offset o over the whole runs of eight in order, lane 0 adds
+// the rest in order, then the eight offset sums in order.
 template <bool FAST>
-__global__ __launch_bounds__(64) void exponentials_kernel(const float *__restrict__ prod, int keys4, float scale,
-                                                          int keys, int pk, float *__restrict__ scores,
-                                                          float *__restrict__ sums)
+__global__ __launch_bounds__(256) void exponentials_kernel(const float *__restrict__ prod, int keys4, float scale,
+                                                           int keys, int pk, float *__restrict__ scores,
+                                                           float *__restrict__ sums)
 {
-    extern __shared__ float row[];
-    const int lane = threadIdx.x;
+    extern __shared__ float row[];  // [pk], then the four waves' maxima
+    float *wmax = row + pk;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t r = blockIdx.x;
     float m = -INFINITY;
-    for (int i = lane; i < pk; i += 64) {
+    for (int i = tid; i < pk; i += 256) {
         const float v = i < keys4 ? prod[r * keys4 + i] * scale : 0.0f;
         row[i] = v;
         if (i < keys) m = fmaxf(m, v);
     }
     for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
-    for (int i = lane; i < keys; i += 64) row[i] = FAST ? ref_exp_fast(row[i] - m) : ref_exp(row[i] - m);
+    if (lane == 0) wmax[wave] = m;
     __syncthreads();
-    const int whole = keys / 8 * 8;
-    float part = 0.0f;
-    if (lane < 8) {
-        // sixteen reads out before their sixteen additions, in run order
-        int i = lane;
-        for (; i + 8 * 15 < whole; i += 8 * 16) {
-            float v[16];
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    for (int i = tid; i < keys; i += 256) row[i] = FAST ? ref_exp_fast(row[i] - m) : ref_exp(row[i] - m);
+    __syncthreads();
+    if (wave == 0) {
+        const int whole = keys / 8 * 8;
+        float part = 0.0f;
+        if (lane < 8) {
+            // sixteen reads out before their sixteen additions, in run order
+            int i = lane;
+            for (; i + 8 * 15 < whole; i += 8 * 16) {
+                float v[16];
 #pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = row[i + 8 * u];
+                for (int u = 0; u < 16; u++) v[u] = row[i + 8 * u];
 #pragma unroll
-            for (int u = 0; u < 16; u++) part = part + v[u];
+                for (int u = 0; u < 16; u++) part = part + v[u];
+            }
+            for (; i < whole; i += 8) part = part + row[i];
         }
-        for (; i < whole; i += 8) part = part + row[i];
-    }
-    float total = -0.0f;
-    if (lane == 0) {
-        for (int i = whole; i < keys; i++) total = total + row[i];
-    }
+        float total = -0.0f;
+        if (lane == 0) {
+            for (int i = whole; i < keys; i++) total = total + row[i];
+        }
 #pragma unroll
-    for (int o = 0; o < 8; o++) {
-        const float po = __shfl(part, o, 64);
-        if (lane == 0) total = total + po;
+        for (int o = 0; o < 8; o++) {
+            const float po = __shfl(part, o, 64);
+            if (lane == 0) total = total + po;
+        }
+        if (lane == 0) sums[r] = total;
     }
-    if (lane == 0) sums[r] = total;
-    for (int i = lane; i < pk; i += 64) scores[r * pk + i] = row[i];
+    for (int i = tid; i < pk; i += 256) scores[r * pk + i] = row[i];
 }
 
 // out[(first + r) · stride + d] = prod[r][d] / sums[r]
@@ -213,10 +220,10 @@ int run(const fg_attention *c, float *out, hipStream_t st, Scratch &w)
                 a.ld_out = size_t(keys4);
                 if ((rc = launch_product(a, st))) return rc;
                 if (c->exponentials == FG_EXP_FAST)
-                    exponentials_kernel<true><<<unsigned(queries), 64, size_t(pk) * 4, st>>>(w.prod, keys4, scale, keys, pk,
+                    exponentials_kernel<true><<<unsigned(queries), 256, size_t(pk) * 4 + 16, st>>>(w.prod, keys4, scale, keys, pk,
                                                                                             w.scores, w.sums);
                 else
-                    exponentials_kernel<false><<<unsigned(queries), 64, size_t(pk) * 4, st>>>(w.prod, keys4, scale, keys, pk,
+                    exponentials_kernel<false><<<unsigned(queries), 256, size_t(pk) * 4 + 16, st>>>(w.prod, keys4, scale, keys, pk,
                                                                                              w.scores, w.sums);
                 FG_HIP(hipGetLastError());
                 ProductArgs b{};

@@ -165,6 +165,21 @@ __global__ void divide_kernel(const float *__restrict__ prod, const float *__res
 
 unsigned blocks_for(size_t n) { return unsigned((n + kThreads - 1) / kThreads); }
 
+// A query row per workgroup; a row of 16384 keys takes 64 KiB and 16 bytes of LDS, past the
+// default limit, which is then raised for the kernel on the current device.
+template <bool FAST>
+int launch_exponentials(const float *prod, int keys4, float scale, int keys, int pk, float *scores, float *sums,
+                        unsigned queries, hipStream_t st)
+{
+    const size_t smem = size_t(pk) * 4 + 16;
+    if (smem > 64 * 1024)
+        FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(exponentials_kernel<FAST>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    exponentials_kernel<FAST><<<queries, 256, smem, st>>>(prod, keys4, scale, keys, pk, scores, sums);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
 struct Scratch {
     float *mean = nullptr, *krows = nullptr, *vrows = nullptr, *qrows = nullptr, *prod = nullptr, *scores = nullptr,
           *sums = nullptr;
@@ -219,13 +234,10 @@ int run(const fg_attention *c, float *out, hipStream_t st, Scratch &w)
                 a.out = w.prod;
                 a.ld_out = size_t(keys4);
                 if ((rc = launch_product(a, st))) return rc;
-                if (c->exponentials == FG_EXP_FAST)
-                    exponentials_kernel<true><<<unsigned(queries), 256, size_t(pk) * 4 + 16, st>>>(w.prod, keys4, scale, keys, pk,
-                                                                                            w.scores, w.sums);
-                else
-                    exponentials_kernel<false><<<unsigned(queries), 256, size_t(pk) * 4 + 16, st>>>(w.prod, keys4, scale, keys, pk,
-                                                                                             w.scores, w.sums);
-                FG_HIP(hipGetLastError());
+                rc = c->exponentials == FG_EXP_FAST
+                         ? launch_exponentials<true>(w.prod, keys4, scale, keys, pk, w.scores, w.sums, unsigned(queries), st)
+                         : launch_exponentials<false>(w.prod, keys4, scale, keys, pk, w.scores, w.sums, unsigned(queries), st);
+                if (rc) return rc;
                 ProductArgs b{};
                 b.t = w.values;
                 b.x = w.scores;

@@ -238,6 +238,13 @@ int fg_matmul(const fg_table *t, const fg_input *in, size_t rows, size_t col_beg
     a.ld_out = ld_out;
     a.accumulate = (flags & FG_ACCUMULATE) != 0;
     a.fused = (flags & FG_FUSED_SCALE) != 0;
+    a.parallel = (flags & FG_PARALLEL_SUM) != 0;
+    if (flags & ~(FG_ACCUMULATE | FG_FUSED_SCALE | FG_PARALLEL_SUM)) return set_error(FG_ERR_ARG, "fg_matmul: unknown flags");
+    if (a.parallel) {
+        if (a.fused) return set_error(FG_ERR_ARG, "fg_matmul: FG_PARALLEL_SUM and FG_FUSED_SCALE exclude each other");
+        if (t->dtype == FG_T2B128) return set_error(FG_ERR_FORMAT, "fg_matmul: FG_PARALLEL_SUM takes Q7b32, Q8b32 and Q4b32 tables");
+        if (rows > 1) return set_error(FG_ERR_SHAPE, "fg_matmul: FG_PARALLEL_SUM takes one row");
+    }
     return launch_product(a, as_stream(stream));
 }
 

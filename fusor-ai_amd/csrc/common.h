@@ -317,7 +317,14 @@ struct ProductArgs {
     int accumulate;
     int32_t *dots;  // when set, the int32 group accumulators are written instead of out
     int fused;      // FG_FUSED_SCALE: s = fma((float)D, ws·as, s)
+    int parallel;   // FG_PARALLEL_SUM: one row, group terms summed as a tree (the decoder's order)
+    // scratch the caller provides (fg_matmul_noalloc): used instead of the workspace pool, never
+    // allocated or freed; a product that needs more than `workspace_bytes` fails
+    void *workspace;
+    size_t workspace_bytes;
 };
+// Scratch bytes a product needs beyond its inputs and outputs (0 for the matrix-vector rows).
+size_t product_scratch_bytes(const ProductArgs &a);
 int launch_matvec(const ProductArgs &a, hipStream_t s);
 int launch_gemm(const ProductArgs &a, hipStream_t s);
 int launch_t2(const ProductArgs &a, hipStream_t s);

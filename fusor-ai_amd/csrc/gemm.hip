@@ -790,6 +790,51 @@ hipError_t workspace_alloc(void **ptr, size_t bytes, hipStream_t s)
     return hipMallocFromPoolAsync(ptr, bytes, pool, s);
 }
 
+// The scratch of a product: the levels, scales and corrections of f32 rows it quantizes first, and
+// the block-major copy of the activation scales when a tile's do not fit in LDS. Each part starts
+// on a 256-byte boundary.
+struct ScratchPlan {
+    size_t q_bytes, s_bytes, t_bytes;
+    bool lds;
+    size_t total() const { return q_bytes + 2 * s_bytes + t_bytes; }
+};
+
+ScratchPlan plan_scratch(const ProductArgs &a)
+{
+    const fg_table *t = a.t;
+    const size_t M = a.rows, K = t->cols, G = t->groups;
+    const size_t Mpad = (M + 63) / 64 * 64;
+    ScratchPlan pl{};
+    pl.q_bytes = a.x ? (M * K + 255) / 256 * 256 : 0;
+    pl.s_bytes = a.x ? (M * G * 4 + 255) / 256 * 256 : 0;
+    if (t->dtype == FG_T2B128) {
+        pl.lds = true;
+        return pl;
+    }
+    // The activation scales go to LDS per tile when a tile's fit in 64 KiB and their rows are
+    // whole float4s; otherwise the kernel reads a block-major copy.
+    const bool dots = a.dots != nullptr;
+    pl.lds = !dots && G * 32 * 4 <= 64 * 1024 && G % 4 == 0 && (a.x || (reinterpret_cast<uintptr_t>(a.as) & 15) == 0);
+    pl.t_bytes = (pl.lds || dots) ? 0 : G * Mpad * 4;
+    return pl;
+}
+
+// The caller's scratch when it brings one, else a pool allocation (freed by the caller of this
+// function on the stream once the product is queued).
+hipError_t scratch_for(const ProductArgs &a, size_t bytes, hipStream_t s, void **ws, bool *owned)
+{
+    *ws = nullptr;
+    *owned = false;
+    if (!bytes) return hipSuccess;
+    if (a.workspace) {
+        if (bytes > a.workspace_bytes) return hipErrorInvalidValue;  // checked by the entry point first
+        *ws = a.workspace;
+        return hipSuccess;
+    }
+    *owned = true;
+    return workspace_alloc(ws, bytes, s);
+}
+
 int launch_t2(const ProductArgs &a, hipStream_t s)
 {
     const fg_table *t = a.t;
@@ -799,10 +844,12 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
     const float *as = a.as;
     const int32_t *corr = a.corr;
     void *ws = nullptr;
+    bool owned = false;
     int rc = FG_OK;
     if (a.x) {  // quantize the f32 rows first (groups of 128)
-        const size_t qb = (size_t(M) * K + 255) / 256 * 256, sb = (size_t(M) * G * 4 + 255) / 256 * 256;
-        FG_HIP(workspace_alloc(&ws, qb + 2 * sb, s));
+        const ScratchPlan pl = plan_scratch(a);
+        const size_t qb = pl.q_bytes, sb = pl.s_bytes;
+        FG_HIP(scratch_for(a, pl.total(), s, &ws, &owned));
         q = static_cast<int8_t *>(ws);
         float *sc = reinterpret_cast<float *>(static_cast<char *>(ws) + qb);
         int32_t *co = reinterpret_cast<int32_t *>(static_cast<char *>(ws) + qb + sb);
@@ -818,7 +865,7 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) rc = check_hip(e, "t2_product_kernel");
     }
-    if (ws) {
+    if (owned) {
         hipError_t e = hipFreeAsync(ws, s);
         if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
     }
@@ -832,16 +879,13 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
     const int M = int(a.rows), K = int(t->cols), G = int(t->groups);
     const int Mpad = (M + 63) / 64 * 64;
     const bool dots = a.dots != nullptr;
-    // The activation scales go to LDS per tile when a tile's fit in 64 KiB and their rows are
-    // whole float4s; otherwise the kernel reads a block-major copy.
-    const bool lds = !dots && size_t(G) * 32 * 4 <= 64 * 1024 && G % 4 == 0 &&
-                     (a.x || (reinterpret_cast<uintptr_t>(a.as) & 15) == 0);
     // Workspace: levels, scales and corrections (when the input is f32), block-major scales.
-    const size_t q_bytes = a.x ? (size_t(M) * K + 255) / 256 * 256 : 0;
-    const size_t s_bytes = a.x ? (size_t(M) * G * 4 + 255) / 256 * 256 : 0;
-    const size_t t_bytes = (lds || dots) ? 0 : size_t(G) * Mpad * 4;
+    const ScratchPlan pl = plan_scratch(a);
+    const bool lds = pl.lds;
+    const size_t q_bytes = pl.q_bytes, s_bytes = pl.s_bytes, t_bytes = pl.t_bytes;
     void *ws = nullptr;
-    if (q_bytes + s_bytes + t_bytes) FG_HIP(workspace_alloc(&ws, q_bytes + 2 * s_bytes + t_bytes, s));
+    bool owned = false;
+    FG_HIP(scratch_for(a, pl.total(), s, &ws, &owned));
     int8_t *q = const_cast<int8_t *>(a.q);
     const float *as = a.as;
     char *base = static_cast<char *>(ws);
@@ -883,7 +927,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.dots_cols = p.col_end - p.col_begin;
         rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, lds, a.fused != 0, s) : launch_tiles<8>(p, dots, lds, a.fused != 0, s);
     }
-    if (ws) {
+    if (owned) {
         hipError_t e = hipFreeAsync(ws, s);
         if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
     }
@@ -892,13 +936,24 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
 
 // Rows 1..4 stream the weights once through the matrix-vector kernel; more rows (and the fused
 // scaling) go to the matrix cores.
+static bool on_matvec(const ProductArgs &a)
+{
+    // the matrix-vector kernel sums separately rounded terms; the fused scaling runs on the tiles
+    return a.t->dtype != FG_T2B128 && a.rows <= 4 && !a.fused;
+}
+
 int launch_product(const ProductArgs &a, hipStream_t s)
 {
     if (a.rows == 0 || a.quad_end <= a.quad_begin) return FG_OK;
     if (a.t->dtype == FG_T2B128) return launch_t2(a, s);
-    // the matrix-vector kernel sums separately rounded terms; the fused scaling runs on the tiles
-    if (a.rows <= 4 && !a.fused) return launch_matvec(a, s);
+    if (on_matvec(a)) return launch_matvec(a, s);
     return launch_gemm(a, s);
+}
+
+size_t product_scratch_bytes(const ProductArgs &a)
+{
+    if (a.rows == 0 || a.quad_end <= a.quad_begin || on_matvec(a)) return 0;
+    return plan_scratch(a).total();
 }
 
 }  // namespace fg

@@ -10,29 +10,35 @@ int launch_proj_q4(const ProjParams &p, int in, int out, bool exact, int nb, siz
 namespace {
 
 template <int FMT, int R, int NB = 8>
-int dispatch_generic(const ProjParams &p, int in, bool dots, size_t smem, unsigned grid, hipStream_t s)
+int dispatch_generic(const ProjParams &p, int in, bool dots, bool tree, size_t smem, unsigned grid, hipStream_t s)
 {
     if (dots) return in == IN_F32 ? launch_one<FMT, R, IN_F32, OUT_DOTS, false>(p, smem, grid, s)
                                   : launch_one<FMT, R, IN_PREQ, OUT_DOTS, false>(p, smem, grid, s);
+    if constexpr (R == 1) {
+        // FG_PARALLEL_SUM: the decoder's parallel-order sums of the same terms
+        if (tree) return in == IN_F32 ? launch_one<FMT, 1, IN_F32, OUT_STORE, false, NB, true>(p, smem, grid, s)
+                                      : launch_one<FMT, 1, IN_PREQ, OUT_STORE, false, NB, true>(p, smem, grid, s);
+    }
     return in == IN_F32 ? launch_one<FMT, R, IN_F32, OUT_STORE, false, NB>(p, smem, grid, s)
                         : launch_one<FMT, R, IN_PREQ, OUT_STORE, false, NB>(p, smem, grid, s);
 }
 
 // One row takes the batch depth its workgroups' shares need (batch_depth), more rows 8 chunks.
 template <int FMT>
-int dispatch_rows(const ProjParams &p, int rows, int in, bool dots, int nb, size_t smem, unsigned grid, hipStream_t s)
+int dispatch_rows(const ProjParams &p, int rows, int in, bool dots, bool tree, int nb, size_t smem, unsigned grid,
+                  hipStream_t s)
 {
     switch (rows) {
     case 1:
         switch (nb) {
-        case 1: return dispatch_generic<FMT, 1, 1>(p, in, dots, smem, grid, s);
-        case 2: return dispatch_generic<FMT, 1, 2>(p, in, dots, smem, grid, s);
-        case 4: return dispatch_generic<FMT, 1, 4>(p, in, dots, smem, grid, s);
-        default: return dispatch_generic<FMT, 1>(p, in, dots, smem, grid, s);
+        case 1: return dispatch_generic<FMT, 1, 1>(p, in, dots, tree, smem, grid, s);
+        case 2: return dispatch_generic<FMT, 1, 2>(p, in, dots, tree, smem, grid, s);
+        case 4: return dispatch_generic<FMT, 1, 4>(p, in, dots, tree, smem, grid, s);
+        default: return dispatch_generic<FMT, 1>(p, in, dots, tree, smem, grid, s);
         }
-    case 2: return dispatch_generic<FMT, 2>(p, in, dots, smem, grid, s);
-    case 3: return dispatch_generic<FMT, 3>(p, in, dots, smem, grid, s);
-    default: return dispatch_generic<FMT, 4>(p, in, dots, smem, grid, s);
+    case 2: return dispatch_generic<FMT, 2>(p, in, dots, false, smem, grid, s);
+    case 3: return dispatch_generic<FMT, 3>(p, in, dots, false, smem, grid, s);
+    default: return dispatch_generic<FMT, 4>(p, in, dots, false, smem, grid, s);
     }
 }
 
@@ -142,8 +148,9 @@ int launch_matvec(const ProductArgs &a, hipStream_t s)
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
     const unsigned grid = unsigned((nq + qpw - 1) / qpw);
     const int nb = batch_depth(p, t->dtype, out);
-    if (t->dtype == FG_Q4B32) return dispatch_rows<4>(p, rows, in, a.dots != nullptr, nb, smem, grid, s);
-    return dispatch_rows<8>(p, rows, in, a.dots != nullptr, nb, smem, grid, s);
+    const bool tree = a.parallel && rows == 1 && !a.dots;
+    if (t->dtype == FG_Q4B32) return dispatch_rows<4>(p, rows, in, a.dots != nullptr, tree, nb, smem, grid, s);
+    return dispatch_rows<8>(p, rows, in, a.dots != nullptr, tree, nb, smem, grid, s);
 }
 
 }  // namespace fg

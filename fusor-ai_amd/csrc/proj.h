@@ -49,6 +49,7 @@ struct ProjParams {
     // new key's own state (rotated query in qkv_out, key and value at the position in the caches)
     const float *part;
     int chunks;
+    float *merged_out;  // when set, workgroup 0 also writes the merged f32 row (an inspection)
     // store
     const float *bias;
     float *out;

@@ -298,6 +298,7 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         }
         const float inv_L = 1.0f / L;
         const v4f merged[1] = {o * inv_L};
+        if (p.merged_out && blockIdx.x == 0 && tid < K / 4) reinterpret_cast<v4f *>(p.merged_out)[tid] = merged[0];
         quantize_slots<1>(merged, K / 4, p.zp, act_q, act_s, act_c);
     } else {
         // rms_norm (ops.rs:7-16): mean of squares, 1/sqrt(mean + eps), x·inverse·weight; then the
@@ -926,14 +927,11 @@ template <int FMT, int R, int IN, int OUT, bool EXACT, int NB = 8, bool TREE = f
 int launch_one(const ProjParams &p, size_t smem, unsigned grid, hipStream_t s)
 {
     auto kernel = proj_kernel<FMT, R, IN, OUT, EXACT, NB, TREE, HD>;
-    if (smem > 64 * 1024) {
-        static bool raised = false;
-        if (!raised) {
-            FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024));
-            raised = true;
-        }
-    }
+    // past 64 KiB of LDS the kernel's limit is raised on the current device, every time (a host
+    // call with no stream work: no per-device state to keep, safe from concurrent callers)
+    if (smem > 64 * 1024)
+        FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   160 * 1024));
     kernel<<<grid, kThreads, smem, s>>>(p);
     FG_HIP(hipGetLastError());
     return FG_OK;

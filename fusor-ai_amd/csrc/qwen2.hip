@@ -49,6 +49,7 @@ struct AttnParams {
     int8_t *q;
     float *scales;
     int32_t *corr;
+    float *row_out;  // when set, the f32 attention row before its quantization (an inspection)
 };
 
 // Scores of every query head of one KV head against kScoreKeys keys (ops.rs:310-326):
@@ -245,6 +246,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
             for (int s2 = 1; s2 < slices; s2++) v = v + parts[s2 * kWeighDims + sub * 4 + e];
             x[e] = v;
         }
+        if (a.row_out) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) a.row_out[head * D + d0 + sub * 4 + e] = x[e];
+        }
         float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
         amax = max8(fmaxf(0.0f, amax));
         int l0, l1, l2, l3;
@@ -416,7 +421,8 @@ int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t positi
 // 3. and 5. a projection added to the residual row: of the attention's output (o: quantized by
 // the attention, or merged from its chunks and the new key and quantized in the prologue), or of
 // the silu(gate)·up row quantized by the SwiGLU epilogue (down).
-int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st, size_t li = 0, size_t position = 0)
+int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st, size_t li = 0, size_t position = 0,
+                    float *merged_out = nullptr)
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(t);
@@ -433,6 +439,7 @@ int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st, size
         p.layer_base = li * sh.kv_heads * sh.capacity * sh.head_dim;
         p.capacity = int(sh.capacity);
         p.position = int(position);
+        p.merged_out = merged_out;
     } else {
         p.q = m->xq;
         p.as = m->xs;
@@ -463,7 +470,7 @@ int swiglu_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, hipStream_t st)
     return launch_proj(p, sh.dtype, IN_NORM, OUT_SWIGLU, sh.exact != 0, st);
 }
 
-int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
+int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st, float *row_out = nullptr)
 {
     const fg_qwen2_shape &sh = m->shape;
     AttnParams a{};
@@ -481,6 +488,7 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st)
     a.q = m->xq;
     a.scales = m->xs;
     a.corr = m->xc;
+    a.row_out = row_out;
     const dim3 sgrid(unsigned(sh.kv_heads), unsigned((a.keys + kScoreKeys - 1) / kScoreKeys));
     attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
     FG_HIP(hipGetLastError());
@@ -633,6 +641,30 @@ extern "C" int fg_qwen2_layer_forward(fg_qwen2 *m, size_t layer, size_t position
     int rc = run_layer(m, layer, position, st);
     if (rc) return rc;
     FG_HIP(hipMemcpyAsync(hidden, m->hidden, m->shape.hidden * 4, hipMemcpyDeviceToDevice, st));
+    return FG_OK;
+}
+
+extern "C" int fg_qwen2_attention(fg_qwen2 *m, size_t layer, size_t position, const float *hidden, float *query, float *row,
+                                  void *stream)
+{
+    if (!m || !hidden || !query || !row) return set_error(FG_ERR_ARG, "fg_qwen2_attention: a null argument");
+    if (layer >= m->shape.layers || position >= m->shape.capacity)
+        return set_error(FG_ERR_SHAPE, "fg_qwen2_attention: layer or position out of range");
+    const fg_qwen2_shape &sh = m->shape;
+    const fg_qwen2_layer &ly = m->layers[layer];
+    hipStream_t st = as_stream(stream);
+    FG_HIP(hipMemcpyAsync(m->hidden, hidden, sh.hidden * 4, hipMemcpyDeviceToDevice, st));
+    int rc;
+    if (fast_attention(m)) {
+        // the chunks, then their merge in the output projection's prologue (which also writes the
+        // projection to the model's own hidden row, not the caller's)
+        if ((rc = qattn_launch(m, ly, layer, position, st))) return rc;
+        if ((rc = residual_launch(m, ly.o, IN_ATTN, st, layer, position, row))) return rc;
+    } else {
+        if ((rc = qkv_launch(m, ly, layer, position, st))) return rc;
+        if ((rc = attention_launch(m, layer, position, st, row))) return rc;
+    }
+    FG_HIP(hipMemcpyAsync(query, m->qkv, sh.heads * sh.head_dim * 4, hipMemcpyDeviceToDevice, st));
     return FG_OK;
 }
 

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "libfusor_gpu.so")
 FG_OK, FG_ERR_SHAPE, FG_ERR_FORMAT, FG_ERR_HIP, FG_ERR_NOMEM, FG_ERR_ARG = range(6)
 FG_ACCUMULATE = 1
 FG_FUSED_SCALE = 2
+FG_PARALLEL_SUM = 4
 
 _P = ctypes.c_void_p
 _S = ctypes.c_size_t
@@ -66,6 +67,7 @@ SIGNATURES = {
     "fg_qwen2_create": (_I, [ctypes.POINTER(FgQwen2Shape), _P, _P, _P, _P, _P, ctypes.POINTER(_P)]),
     "fg_qwen2_step": (_I, [_P, _I, _S, _P, _P, _P, _P]),
     "fg_qwen2_layer_forward": (_I, [_P, _S, _S, _P, _P]),
+    "fg_qwen2_attention": (_I, [_P, _S, _S, _P, _P, _P, _P]),
     "fg_qwen2_free": (_I, [_P]),
 }
 

@@ -67,6 +67,9 @@ def attend(call, out, stream=None):
     _check_operand("query", c.query, c.images * c.queries, c.heads, c.head_dim)
     _check_operand("key", c.key, c.images * c.keys, c.kv_heads, c.head_dim)
     _check_operand("value", c.value, c.images * c.keys, c.kv_heads, c.head_dim)
+    import torch
+    if out.dtype != torch.float32:
+        raise ShapeError("out must be float32")
     if not out.is_cuda or not out.is_contiguous() or out.numel() < c.images * c.queries * c.heads * c.head_dim:
         raise ShapeError("out: a contiguous device tensor of images * queries rows of heads * head_dim")
     fg = FgAttention(c.heads, c.kv_heads, c.head_dim, c.images, c.queries, c.keys,

@@ -134,13 +134,25 @@ def _check_input(weights, x):
         raise ShapeError("the input is prepared for the weights' format")  # matmul.rs:301-304
 
 
-def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False, fused=False):
+def _check_device_f32(name, t, extent):
+    """A caller's float32 device tensor whose storage holds `extent` values from its first one (a
+    strided view counts the storage behind it), so that the kernels' reads and writes stay in it."""
+    import torch
+    if t.dtype != torch.float32 or t.device.type != "cuda":
+        raise ShapeError(f"{name} must be a float32 device tensor")
+    room = t.untyped_storage().nbytes() // 4 - t.storage_offset()
+    if room < extent:
+        raise ShapeError(f"{name} holds {room} values from its first, {extent} needed")
+
+
+def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False, fused=False, parallel=False):
     """matmul (matmul.rs:265-276) over output columns `cols` (a range of whole quads).
 
     Returns the device tensor [rows, len(cols)] of results; with `store`, also calls
     store(row, first_col, [4 floats]) per row and quad, in the reference's order. The results are
     the scalar backend's bits, or with `fused` the NEON backend's (each group's total scaled with
-    one fused multiply-add, arch/neon.rs:140-154).
+    one fused multiply-add, arch/neon.rs:140-154). `parallel` (one row) sums each output's group
+    terms as the decoder's parallel order does: the same terms, reordered additions.
     """
     import torch
     if cols.start % QUAD or cols.stop % QUAD:
@@ -150,16 +162,29 @@ def matmul(weights, x, cols, store=None, bias=None, out=None, accumulate=False, 
     width = cols.stop - cols.start
     if out is None:
         out = torch.empty((rows, width), dtype=torch.float32, device="cuda")
+    if out.dim() == 2:
+        if out.shape[1] < width or out.shape[0] < rows or out.stride(1) != 1:
+            raise ShapeError(f"out of shape {list(out.shape)} for {rows} rows of {width} columns")
+        ld = out.stride(0)
+    else:
+        if not out.is_contiguous():
+            raise ShapeError("out must be contiguous")
+        ld = width
+    if rows and width:
+        _check_device_f32("out", out, (rows - 1) * ld + width)
+    if bias is not None:
+        _check_device_f32("bias", bias, min(weights.rows, cols.stop))
     inp = x.ffi()
+    flags = (_lib.FG_ACCUMULATE if accumulate else 0) | (_lib.FG_FUSED_SCALE if fused else 0) | \
+        (_lib.FG_PARALLEL_SUM if parallel else 0)
     check(lib().fg_matmul(weights.table.handle, ctypes.byref(inp), rows, cols.start, cols.stop, ptr(bias), ptr(out),
-                          out.stride(0) if out.dim() == 2 else width,
-                          (_lib.FG_ACCUMULATE if accumulate else 0) | (_lib.FG_FUSED_SCALE if fused else 0),
-                          stream_handle()))
+                          ld, flags, stream_handle()))
     if store is not None:
-        host = out.cpu().numpy()
+        host = out.cpu().numpy().reshape(-1)
         for r in range(rows):
             for first in range(0, width, QUAD):
-                store(r, cols.start + first, host[r, first:first + QUAD].tolist())
+                at = r * ld + first
+                store(r, cols.start + first, host[at:at + QUAD].tolist())
     return out
 
 

@@ -62,3 +62,10 @@ class Qwen2:
 
     def layer_forward(self, layer, position, hidden, stream=None):
         check(lib().fg_qwen2_layer_forward(self.handle, layer, position, ptr(hidden), stream_handle(stream)))
+
+    def attention(self, layer, position, hidden, query, row, stream=None):
+        """One layer's attention over `hidden` as the step runs it (an inspection): the rotated
+        query heads into `query` and the attention's f32 output row into `row` (device tensors of
+        heads * head_dim); the position's key and value are kept in the caches."""
+        check(lib().fg_qwen2_attention(self.handle, layer, position, ptr(hidden), ptr(query), ptr(row),
+                                       stream_handle(stream)))

@@ -47,6 +47,13 @@ extern "C" {
  * separately rounded s + (float)D * (ws * as) (arch/scalar.rs:80-89). Groups stay in order, so the
  * f32 results are the NEON backend's bits. Rows 1..4 then take the matrix cores too. */
 #define FG_FUSED_SCALE 2
+/* One row only: sum each output's group terms fl(fl((float)D) * fl(ws * as)) in parallel, a team of
+ * lanes over strided terms then a lane reduction, instead of in group order. This is the order
+ * fg_qwen2 uses when it is not exact (an inspection of that reduction, not a reference backend):
+ * the terms are the scalar backend's, only their additions are reordered, so each output is
+ * within (G - 1) * 2^-24 * sum_g |term_g| of the scalar backend's (G groups). Not with
+ * FG_FUSED_SCALE, not for T2b128. */
+#define FG_PARALLEL_SUM 4
 
 /* The last failure's message on this thread ("" when none). */
 const char *fg_last_error(void);
@@ -194,6 +201,14 @@ int fg_qwen2_step(fg_qwen2 *model, int token, size_t position, float *hidden, fl
                   int32_t *next_token, void *stream);
 /* One layer over a device hidden row (the residual stream, in and out), for layer-level checks. */
 int fg_qwen2_layer_forward(fg_qwen2 *model, size_t layer, size_t position, float *hidden, void *stream);
+/* An inspection of one layer's attention (layer.rs:175-209, transformer.rs:185-219) over a device
+ * hidden row, as the step runs it: the normed row projected to the query, key and value heads, the
+ * position's key and value kept in the caches, the query heads rotated, then attention over keys
+ * 0..position. Writes the rotated query heads to `query` and the attention's output row (f32, before
+ * the output projection quantizes it) to `row`, both device [heads * head_dim]. `hidden` is not
+ * changed. */
+int fg_qwen2_attention(fg_qwen2 *model, size_t layer, size_t position, const float *hidden, float *query,
+                       float *row, void *stream);
 int fg_qwen2_free(fg_qwen2 *model);
 
 #ifdef __cplusplus

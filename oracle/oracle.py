@@ -263,6 +263,14 @@ def rope_tables(base, head_dim, positions):
     return cos, sin
 
 
+def dot_f32(a, b):
+    """dot_f32 (arch/scalar.rs:340-342): the products added in index order."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    assert a.size == b.size
+    return np.float32(lib().or_dot_f32(_ptr(a), _ptr(b), a.size))
+
+
 def softmax(x):
     x = np.array(x, dtype=np.float32)
     lib().or_softmax(_ptr(x), x.size)

@@ -53,6 +53,9 @@ CASES = [  # heads, kv_heads, head_dim, images, queries, keys, fast
     (4, 2, 40, 2, 37, 53, True),
     (3, 3, 16, 1, 1, 1, False),       # one key, one query
     (8, 2, 128, 1, 64, 1000, False),  # a long row of keys
+    (1, 1, 64, 1, 4, 4096, True),     # the DiT block's 4096 keys, on the matrix-vector kernel
+    (2, 1, 64, 1, 5, 16384, False),   # the largest row of keys: 64 KiB of scores per row in LDS
+    (1, 1, 32, 1, 2, 16384, True),
 ]
 
 

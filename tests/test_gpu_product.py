@@ -75,6 +75,27 @@ def test_encode_matches_the_oracle(fk, dtype):
     assert np.array_equal(got, want)
 
 
+def test_q4_encode_keeps_the_signed_extreme(fk):
+    """Q4b32's scale is the first value of largest magnitude over -8 (quant.rs:151-166), sign
+    included: known answers worked from that rule, where |extreme| or the last extreme would give
+    other codes and scales."""
+    rows, cols = 4, 32
+    values = np.zeros((rows, cols), np.float32)
+    values[0, :4] = [0.5, 8.0, -2.0, 0.0]  # positive extreme: d = -1, 8 -> 0, -2 -> 10, 0.5 -> 8 (-0.5 to even)
+    values[1, :2] = [-8.0, 8.0]            # the first of equal magnitudes: d = 1, -8 -> 0, 8 -> 16 clamped to 15
+    values[2, :2] = [8.0, -8.0]            # the other way round: d = -1, 8 -> 0, -8 -> 15
+    values[3, :3] = [-1.0, 4.0, -3.0]      # d = -0.5: -1 -> 10, 4 -> 0, -3 -> 14
+    got = fk.Tensor.encode(fk.DType.Q4b32, [rows, cols], values).bytes()
+    assert np.array_equal(got, O.encode(O.Q4B32, rows, cols, values))
+    scales = np.ascontiguousarray(got[rows * cols // 2:]).view(np.float32)
+    assert scales.tolist() == [-1.0, 1.0, -1.0, -0.5]
+    codes = [O.unpack_lane(O.Q4B32, got[:64], lane) for lane in range(4)]
+    assert codes[0][:4].tolist() == [8, 0, 10, 8] and codes[0][4:].tolist() == [8] * 28
+    assert codes[1][:2].tolist() == [0, 15]
+    assert codes[2][:2].tolist() == [0, 15]
+    assert codes[3][:3].tolist() == [10, 0, 14]
+
+
 def test_encode_rejects_partial_groups(fk):
     with pytest.raises(fk.FormatError, match=r"a T2b128 tensor of shape \[1, 64\]: a matrix of whole groups of 128 expected"):
         fk.Tensor.encode(fk.DType.T2b128, [1, 64], np.ones(64, np.float32))
@@ -343,18 +364,21 @@ def test_single_matvec_shape_bit_exact(fk, dtype):
     assert np.array_equal(gpu_product(fk, t, x, 1, dots=True), want_dots)
 
 
-@pytest.mark.parametrize("shape", [(512, 896, 9728), (512, 4864, 896), (4096, 1152, 3456), (4096, 4608, 1152)])
-def test_batched_shapes_bit_exact_on_sampled_rows(fk, shape):
-    """Full-size GEMMs; the oracle checks a sample of rows over every column (rows are
-    independent)."""
+@pytest.mark.parametrize("shape", [(512, 896, 9728), (512, 4864, 896), (4096, 1152, 3456), (4096, 1152, 4608),
+                                   (4096, 4608, 1152)])
+def test_batched_shapes_bit_exact_in_full(fk, shape):
+    """The full-size GEMMs (512-row prefill and the 4096-row DiT block's QKV, MLP up and MLP down),
+    every output of every row against the oracle's threaded product: every row tile and column tile
+    of the per-XCD tile order."""
     rows, k, n = shape
-    data = synthetic_table(O.Q8B32, n, k, seed=rows + k)
+    print(f"batched {rows}x{k}->{n}", flush=True)
+    data = synthetic_table(O.Q8B32, n, k, seed=rows + k + n)
     t = table(fk, O.Q8B32, n, k, data)
-    x = (activations(rows, k, seed=k, outliers=0.01) * np.float32(np.sqrt(2.0))).astype(np.float32)
+    x = (activations(rows, k, seed=k + n, outliers=0.01) * np.float32(np.sqrt(2.0))).astype(np.float32)
     got = gpu_product(fk, t, x, rows)
-    sample = [0, 1, 31, 32, 63, rows // 2 + 5, rows - 1]
-    want = oracle_product(O.Q8B32, n, k, data, x[sample], len(sample))
-    assert same_bits(got[sample], want), first_mismatch(got[sample], want)
+    q, s, c = O.quantize_rows(x.reshape(-1), O.Q8B32)
+    want = O.matmul_threaded(O.Q8B32, n, k, data, q, s, c, rows, threads=16)
+    assert same_bits(got, want), first_mismatch(got, want)
 
 
 @pytest.mark.parametrize("rows", [1, 16])

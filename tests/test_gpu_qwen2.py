@@ -142,6 +142,23 @@ def test_decoder_head_sizes_and_many_key_chunks(fk, head_dim, heads, kv_heads):
         assert rel_l2(got[1], want[1]) < FAST_TOLERANCE, ("fast logits", position)
 
 
+def test_decoder_with_rows_of_heads_wider_than_1024(fk):
+    """12 query heads of 128 over 2 key heads: the attention row (1536) is past what the
+    flash-decoding merge takes, so parallel order runs the scores and weighted-sum kernels with
+    eight slices of partial sums and a block-reduced total; positions on both sides of one
+    256-key chunk of values. Exact mode bit-identical, parallel order within tolerance."""
+    shape = dict(hidden=256, layers=2, heads=12, kv_heads=2, head_dim=128, ffn=512, vocab=64, capacity=300)
+    params = build(O.Q7B32, seed=12, synthetic=False, **shape)
+    for position in (200, 255, 256, 299):
+        got, want = run_both(fk, O.Q7B32, params, token=7, position=position, exact=True)
+        assert same_bits(got[0], want[0]), ("hidden", position)
+        assert same_bits(got[1], want[1]), ("logits", position)
+        assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+        got, want = run_both(fk, O.Q7B32, params, token=7, position=position, exact=False)
+        assert rel_l2(got[0], want[0]) < FAST_TOLERANCE, ("fast hidden", position)
+        assert rel_l2(got[1], want[1]) < FAST_TOLERANCE, ("fast logits", position)
+
+
 def test_layer_forward_equals_the_oracle_layer(fk):
     import torch
     dtype = O.Q7B32

@@ -58,6 +58,23 @@ def test_quantized_rows_dequantize_within_one_step(dtype):
             assert np.all(np.abs(got[b * 32:(b + 1) * 32] - block) <= tol + 1e-5)
 
 
+@pytest.mark.parametrize("group,scale,codes", [
+    # the first value of largest magnitude, sign kept, over -8 (quant.rs:151-166), worked by hand:
+    ([0.5, 8.0, -2.0, 0.0], -1.0, [8, 0, 10, 8]),   # positive extreme; 0.5 / -1 rounds to -0
+    ([-8.0, 8.0], 1.0, [0, 15]),                     # the first of equal magnitudes; 16 clamps to 15
+    ([8.0, -8.0], -1.0, [0, 15]),
+    ([-1.0, 4.0, -3.0], -0.5, [10, 0, 14]),
+])
+def test_q4_scale_is_the_signed_first_extreme(group, scale, codes):
+    """Known answers a scale from |extreme|, or from the last extreme, would fail."""
+    values = np.zeros(32, np.float32)
+    values[:len(group)] = group
+    got_scale, got_codes = O.quantize_group(O.Q4B32, values)
+    assert got_scale == np.float32(scale)
+    assert got_codes[:len(codes)].tolist() == codes
+    assert got_codes[len(codes):].tolist() == [8] * (32 - len(codes))
+
+
 def test_a_row_of_subnormal_values_keeps_seven_bit_codes():
     """matmul.rs:845-856: one value of bits 94, the rest zero, codes [127, 64]."""
     row = np.zeros(32, np.float32)

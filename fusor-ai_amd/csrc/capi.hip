@@ -54,6 +54,35 @@ static size_t byte_len(int dtype, size_t rows, size_t cols)
     return padded / size_t(codes_per_byte(dtype)) + padded / size_t(group_of(dtype)) * 4;
 }
 
+size_t table_byte_len(int dtype, size_t rows, size_t cols) { return byte_len(dtype, rows, cols); }
+
+int table_alloc(int dtype, size_t rows, size_t cols, fg_table **out)
+{
+    *out = nullptr;
+    int rc = check_matrix(dtype, rows, cols);
+    if (rc) return rc;
+    fg_table *t = new fg_table();
+    t->dtype = dtype;
+    t->rows = rows;
+    t->cols = cols;
+    t->quads = (rows + 3) / 4;
+    t->blocks = cols / 32;
+    t->groups = cols / size_t(group_of(dtype));
+    t->code_bytes = t->quads * t->blocks * quad_bytes(dtype);
+    t->codes = nullptr;
+    t->scales = nullptr;
+    const size_t scale_bytes = t->quads * t->groups * 4 * 4;
+    hipError_t e = hipMalloc(reinterpret_cast<void **>(&t->codes), std::max<size_t>(t->code_bytes, 16));
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&t->scales), std::max<size_t>(scale_bytes, 16));
+    if (e != hipSuccess) {
+        if (t->codes) (void)hipFree(t->codes);
+        delete t;
+        return check_hip(e, "table storage: hipMalloc");
+    }
+    *out = t;
+    return FG_OK;
+}
+
 static int create(const void *bytes, size_t len, int dtype, size_t rows, size_t cols, void *stream, bool device,
                   fg_table **out)
 {
@@ -68,22 +97,13 @@ static int create(const void *bytes, size_t len, int dtype, size_t rows, size_t 
                                            " expected)");
     if (!bytes && len) return set_error(FG_ERR_ARG, "fg_table_create: null bytes");
     hipStream_t s = as_stream(stream);
-    fg_table *t = new fg_table();
-    t->dtype = dtype;
-    t->rows = rows;
-    t->cols = cols;
-    t->quads = (rows + 3) / 4;
-    t->blocks = cols / 32;
-    t->groups = cols / size_t(group_of(dtype));
-    t->code_bytes = t->quads * t->blocks * quad_bytes(dtype);
-    t->codes = nullptr;
-    t->scales = nullptr;
+    fg_table *t = nullptr;
+    if ((rc = table_alloc(dtype, rows, cols, &t))) return rc;
     uint8_t *staging = nullptr;
     const size_t scale_bytes = t->quads * t->groups * 4 * 4;
-    hipError_t e = hipMalloc(reinterpret_cast<void **>(&t->codes), std::max<size_t>(t->code_bytes, 16));
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&t->scales), std::max<size_t>(scale_bytes, 16));
+    hipError_t e = hipSuccess;
     const uint8_t *ref_codes = static_cast<const uint8_t *>(bytes);
-    if (e == hipSuccess && !device && t->code_bytes) {
+    if (!device && t->code_bytes) {
         e = hipMalloc(reinterpret_cast<void **>(&staging), t->code_bytes);
         if (e == hipSuccess) e = hipMemcpyAsync(staging, bytes, t->code_bytes, hipMemcpyHostToDevice, s);
         ref_codes = staging;
@@ -102,8 +122,8 @@ static int create(const void *bytes, size_t len, int dtype, size_t rows, size_t 
     }
     if (staging) (void)hipFree(staging);
     if (rc) {
-        if (t->codes) (void)hipFree(t->codes);
-        if (t->scales) (void)hipFree(t->scales);
+        (void)hipFree(t->codes);
+        (void)hipFree(t->scales);
         delete t;
         return rc;
     }

@@ -294,6 +294,11 @@ __device__ __forceinline__ int nibbles_signed(int packed_nibbles)
 namespace fg {
 int launch_relayout(const uint8_t *ref_codes, fg_table *t, hipStream_t s);
 int launch_unrelayout(const fg_table *t, uint8_t *ref_codes, hipStream_t s);
+// Reference quad blocks (whole ones, `bytes` long) to device quad blocks at the same offset.
+int launch_relayout_range(const uint8_t *ref_codes, uint8_t *dev_codes, int dtype, size_t bytes, hipStream_t s);
+// A table's device storage for a shape (codes and scales uninitialised), or an error.
+int table_alloc(int dtype, size_t rows, size_t cols, fg_table **out);
+size_t table_byte_len(int dtype, size_t rows, size_t cols);
 int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint8_t *bytes, hipStream_t s);
 int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s);
 int launch_quantize_rows(const float *x, size_t count, int dtype, int8_t *q, float *scales, int32_t *corr,

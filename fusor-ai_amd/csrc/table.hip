@@ -259,6 +259,17 @@ int launch_relayout(const uint8_t *ref_codes, fg_table *t, hipStream_t s)
     return FG_OK;
 }
 
+int launch_relayout_range(const uint8_t *ref_codes, uint8_t *dev_codes, int dtype, size_t bytes, hipStream_t s)
+{
+    // whole quad blocks: the transpose never leaves one, so any run of them relays on its own
+    const size_t n = bytes / 4;
+    if (n == 0) return FG_OK;
+    relayout_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint32_t *>(ref_codes),
+                                                              reinterpret_cast<uint32_t *>(dev_codes), dtype, n, 0);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
 int launch_unrelayout(const fg_table *t, uint8_t *ref_codes, hipStream_t s)
 {
     const size_t n = t->code_bytes / 4;

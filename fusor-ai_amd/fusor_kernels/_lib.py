@@ -53,6 +53,11 @@ SIGNATURES = {
     "fg_table_shape": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_S), ctypes.POINTER(_S)]),
     "fg_table_byte_len": (_S, [_I, _S, _S]),
     "fg_table_read": (_I, [_P, _P, _P]),
+    "fg_upload_begin": (_I, [_I, _S, _S, _P, ctypes.POINTER(_P)]),
+    "fg_upload_write": (_I, [_P, _S, _P, _S]),
+    "fg_upload_end": (_I, [_P, ctypes.POINTER(_P)]),
+    "fg_upload_restart": (_I, [_P]),
+    "fg_upload_free": (_I, [_P]),
     "fg_encode": (_I, [_I, _S, _S, _P, _P, _P]),
     "fg_dequantize_row": (_I, [_P, _S, _P, _P]),
     "fg_qmatrix_create": (_I, [_S, _S, ctypes.POINTER(_P)]),

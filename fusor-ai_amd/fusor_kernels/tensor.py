@@ -183,6 +183,55 @@ class Table:
         return out
 
 
+class TableUpload:
+    """A quantized table streamed onto the device piece by piece, as bundle::Store::write receives
+    a part's bytes (bundle/src/store.rs:90-126), then handed over as a `Table` once every byte came
+    (Store::end_part, store.rs:129-146; Table::load, bundle/src/load.rs:72-84)."""
+
+    def __init__(self, dtype, shape, stream=None):
+        dtype = DType(dtype)
+        fmt = dtype.quant_format()
+        if fmt is None or len(shape) != 2:
+            raise FormatError(f"a {dtype.name} tensor of shape {list(shape)}: a quantized matrix expected")
+        _check_quantized(fmt, shape)
+        handle = ctypes.c_void_p()
+        check(lib().fg_upload_begin(int(dtype), shape[0], shape[1], stream_handle(stream), ctypes.byref(handle)))
+        self.handle, self._dtype, self._shape = handle, dtype, list(shape)
+        self.received = 0
+        self.len = byte_len(dtype, shape)
+
+    def write(self, piece):
+        """The next bytes (anything exposing the buffer protocol: bytes, a numpy uint8 array...)."""
+        view = memoryview(piece).cast("B")
+        n = view.nbytes
+        if n:
+            buf = (ctypes.c_ubyte * n).from_buffer_copy(view) if view.readonly else (ctypes.c_ubyte * n).from_buffer(view)
+            check(lib().fg_upload_write(self.handle, self.received, buf, n))
+        else:
+            check(lib().fg_upload_write(self.handle, self.received, None, 0))
+        self.received += n
+
+    def restart(self):
+        check(lib().fg_upload_restart(self.handle))
+        self.received = 0
+
+    def end(self):
+        """The table, once every byte was written."""
+        out = ctypes.c_void_p()
+        check(lib().fg_upload_end(self.handle, ctypes.byref(out)))
+        self.handle = None
+        t = Table.__new__(Table)
+        t.handle, t._dtype = out, self._dtype
+        t.rows, t.cols = self._shape
+        return t
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and _lib._lib is not None:
+            _lib._lib.fg_upload_free(h)
+            self.handle = None
+
+
 class Matrix:
     """A borrowed [rows, cols] view of a table (tensor.rs:65-81)."""
 

@@ -82,6 +82,31 @@ int fg_table_shape(const fg_table *table, int *dtype, size_t *rows, size_t *cols
 size_t fg_table_byte_len(int dtype, size_t rows, size_t cols);
 int fg_table_read(const fg_table *table, void *bytes, void *stream);
 
+/* A table streamed onto the device as a bundle store receives its bytes, instead of from one whole
+ * byte array: the device side of Store::write's copy into a zeroed tensor (bundle/src/store.rs:90-126),
+ * Store::end_part's size check (store.rs:129-146) and Table::load (bundle/src/load.rs:72-84). A Store
+ * routes each piece of a part to its tensor (store.rs:105-124); for a quantized table the binding
+ * passes the piece here instead of into Tensor::bytes_mut. One upload is used by one thread at a
+ * time. */
+typedef struct fg_upload fg_upload;
+/* Store::new's zeroed tensor (store.rs:49-61) for a quantized [rows, cols] table: its device storage
+ * and two pinned staging buffers. Every copy of the upload runs on `stream`. */
+int fg_upload_begin(int dtype, size_t rows, size_t cols, void *stream, fg_upload **out);
+/* The next `len` host bytes of the table's reference bytes (tensor.rs:1-9), at byte `offset` of the
+ * table: writes arrive in order, so `offset` is the count of bytes written so far (FG_ERR_SHAPE
+ * otherwise); past the table's byte length, FG_ERR_FORMAT "table upload: write past its end"
+ * (store.rs:95-97). Pieces of any size, zero included. */
+int fg_upload_write(fg_upload *upload, size_t offset, const void *bytes, size_t len);
+/* Every byte written (else FG_ERR_FORMAT "table upload: N of M bytes", store.rs:130-137, and the
+ * upload stays open): waits for the last copies and hands over the table, which fg_table_free
+ * frees. The upload is consumed on success. */
+int fg_upload_end(fg_upload *upload, fg_table **out);
+/* Store::restart_part (store.rs:148-158): forgets what was written, so the table is written again
+ * from byte 0. */
+int fg_upload_restart(fg_upload *upload);
+/* Drops an upload that did not end, with its device storage. */
+int fg_upload_free(fg_upload *upload);
+
 /* Tensor::encode of a quantized [rows, cols] matrix (tensor.rs:97-143, quant.rs:143-177):
  * device f32 `values` (row-major) to device `bytes` (fg_table_byte_len long) in the reference
  * layout. */

@@ -3,11 +3,40 @@
 // GPU kernels do not cover returns an error.
 #include <algorithm>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "common.h"
 
 namespace fg {
+
+// fg_matmul_noalloc's scratch: one array per device, held from the library's load until the
+// process ends (each GPU the library runs on keeps its own copy at its own address). Host code
+// never uses the array's name as an address: its device address comes from hipGetSymbolAddress,
+// once per device, with that device current.
+constexpr size_t kNoAllocScratch = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
+
+// The device address of this device's scratch array (looked up on the device's first call).
+static int scratch_address(void **out)
+{
+    static std::mutex mu;
+    static void *address[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return check_hip(e, "fg_matmul_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= 64) return set_error(FG_ERR_ARG, "fg_matmul_noalloc: device index past 63");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!address[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return check_hip(e, "fg_matmul_noalloc: hipGetSymbolAddress");
+        if (!ptr) return set_error(FG_ERR_HIP, "fg_matmul_noalloc: no device address for the scratch array");
+        address[dev] = ptr;
+    }
+    *out = address[dev];
+    return FG_OK;
+}
 
 static thread_local std::string g_last_error;
 
@@ -264,6 +293,32 @@ int fg_matmul(const fg_table *t, const fg_input *in, size_t rows, size_t col_beg
         if (a.fused) return set_error(FG_ERR_ARG, "fg_matmul: FG_PARALLEL_SUM and FG_FUSED_SCALE exclude each other");
         if (t->dtype == FG_T2B128) return set_error(FG_ERR_FORMAT, "fg_matmul: FG_PARALLEL_SUM takes Q7b32, Q8b32 and Q4b32 tables");
         if (rows > 1) return set_error(FG_ERR_SHAPE, "fg_matmul: FG_PARALLEL_SUM takes one row");
+    }
+    return launch_product(a, as_stream(stream));
+}
+
+int fg_matmul_noalloc(const fg_table *t, const fg_input *in, size_t rows, size_t col_begin, size_t col_end, const float *bias,
+                      float *out, size_t ld_out, int flags, void *stream)
+{
+    int rc = check_product(t, in, rows, col_begin, col_end, "fg_matmul_noalloc");
+    if (rc) return rc;
+    if (!out && rows && col_end > col_begin) return set_error(FG_ERR_ARG, "fg_matmul_noalloc: a null output");
+    if (ld_out < col_end - col_begin) return set_error(FG_ERR_SHAPE, "fg_matmul_noalloc: ld_out shorter than the columns");
+    if (flags & ~(FG_ACCUMULATE | FG_FUSED_SCALE)) return set_error(FG_ERR_ARG, "fg_matmul_noalloc: unknown flags");
+    ProductArgs a = product_args(t, in, rows, col_begin, col_end);
+    a.bias = bias;
+    a.out = out;
+    a.ld_out = ld_out;
+    a.accumulate = (flags & FG_ACCUMULATE) != 0;
+    a.fused = (flags & FG_FUSED_SCALE) != 0;
+    const size_t need = product_scratch_bytes(a);
+    if (need > kNoAllocScratch)
+        return set_error(FG_ERR_SHAPE, "fg_matmul_noalloc: this product needs " + std::to_string(need) +
+                                           " bytes of scratch, more than the " + std::to_string(kNoAllocScratch) +
+                                           " the library holds (use fg_matmul)");
+    if (need) {
+        if ((rc = scratch_address(&a.workspace))) return rc;
+        a.workspace_bytes = kNoAllocScratch;
     }
     return launch_product(a, as_stream(stream));
 }

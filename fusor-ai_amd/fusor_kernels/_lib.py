@@ -68,6 +68,7 @@ SIGNATURES = {
     "fg_attend": (_I, [ctypes.POINTER(FgAttention), _P, _P]),
     "fg_quantize_rows": (_I, [_P, _S, _I, _P, _P, _P, _P]),
     "fg_matmul": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P, _S, _I, _P]),
+    "fg_matmul_noalloc": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P, _S, _I, _P]),
     "fg_matmul_dots": (_I, [_P, ctypes.POINTER(FgInput), _S, _S, _S, _P, _P]),
     "fg_qwen2_create": (_I, [ctypes.POINTER(FgQwen2Shape), _P, _P, _P, _P, _P, ctypes.POINTER(_P)]),
     "fg_qwen2_step": (_I, [_P, _I, _S, _P, _P, _P, _P]),

@@ -189,6 +189,18 @@ typedef struct {
 int fg_matmul(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
               size_t col_end, const float *bias, float *out, size_t ld_out, int flags, void *stream);
 
+/* fg_matmul that allocates nothing. No counterpart in the reference (whose CPU product needs no
+ * scratch): it is for callers that cannot allocate device memory, such as code under HIP graph
+ * capture or a serving loop that forbids hipMalloc. Products that quantize f32 rows on the matrix
+ * cores (5 or more rows, or T2b128) need scratch for the levels, scales and corrections; here it is
+ * a fixed array of 32 MiB per device, held by the library from its load until the process ends
+ * (rows * cols + 8 * rows * groups bytes, each part rounded up to 256, must fit; larger products
+ * return FG_ERR_SHAPE and belong to fg_matmul). Nothing in the array needs to start at zero: every
+ * call writes what it reads. All calls on one device share the array, so calls that overlap on a
+ * device (other threads or streams) race: serialize them. FG_PARALLEL_SUM is not taken. */
+int fg_matmul_noalloc(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
+                      size_t col_end, const float *bias, float *out, size_t ld_out, int flags, void *stream);
+
 /* The int32 group accumulators of the same product (the dots of matmul.rs:671-709, correction
  * included): dots[(r * (col_end - col_begin) + (c - col_begin)) * groups + g]. An inspection
  * entry point for parity checks. */

@@ -18,6 +18,7 @@
 #include "common.h"
 
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 
 namespace fg {
@@ -25,6 +26,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 struct GemmParams {
     const int8_t *codes;
@@ -648,6 +650,186 @@ __global__ __launch_bounds__(256) void gemm16_split_kernel(GemmParams p)
     *o = p.accumulate ? *o + y : y;
 }
 
+// LDS-staged tiles for the products with many tiles (the 4096-row DiT block, 512-row prefill with
+// wide outputs). A workgroup of four waves owns a (64·WM) x (64·WN) output tile; wave w owns the
+// 32·WM x 32·WN sub-tile (w / 2, w % 2): WM x WN MFMA tiles of 32 x 32. The workgroup's operands
+// for kStageBlocks blocks at a time (a stage) are staged in LDS once and read by every wave:
+//   A  [kb][BM rows][32 B]   int8 activation levels (q, row-major [M][K]);
+//   W  [kb][BN cols][32 B]   weight levels (Q8; Q4: [kb][BN cols][16 B] packed nibbles);
+//   AS [kb][BM]              activation scales, from the block-major copy as_t [G][Mpad];
+//   WS [kb][BN/4 quads][4]   weight scales, the table's own order ((q·G + g)·4 + lane).
+// Every stage arrives by direct global-to-LDS loads (global_load_lds_dwordx4: lane l writes 16 bytes
+// at base + 16·l), so no register holds staged data and the loads take no VALU work. Two stage
+// buffers: stage s + 1 is loaded while stage s is multiplied; one barrier per stage both publishes
+// stage s and frees the buffer of stage s - 1. Rows and columns past the edges re-read the last
+// valid one (in bounds, never stored); blocks past the last one are loaded clamped and skipped.
+// Per block each wave issues its WM·WN MFMAs, then adds each output's term in group order, the
+// reference's sum to the bit (or the NEON backend's fused form).
+constexpr int kStageBlocks = 2;
+
+template <int FMT, int WM, int WN>
+struct LdsTile {
+    static constexpr int BM = 64 * WM, BN = 64 * WN, KB = kStageBlocks;
+    static constexpr int RB = FMT == 8 ? 32 : 16;  // bytes of a weight row-block on the device
+    static constexpr int A_BYTES = KB * BM * 32, W_BYTES = KB * BN * RB, AS_BYTES = KB * BM * 4, WS_BYTES = KB * BN * 4;
+    static constexpr int STAGE = A_BYTES + W_BYTES + AS_BYTES + WS_BYTES;
+    static constexpr int A_LOADS = A_BYTES / 1024, W_LOADS = W_BYTES / 1024;
+    static constexpr int AS_LANES = AS_BYTES / 16, WS_LANES = WS_BYTES / 16;  // 16 bytes per lane
+    static_assert(A_BYTES % 1024 == 0 && W_BYTES % 1024 == 0 && AS_LANES <= 64 && WS_LANES <= 64, "stage shape");
+};
+
+template <int FMT, int WM, int WN, bool FUSED>
+__global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p)
+{
+    using T = LdsTile<FMT, WM, WN>;
+    constexpr int BM = T::BM, BN = T::BN, KB = T::KB, RB = T::RB;
+    constexpr int QB = FMT == 8 ? 128 : 64;  // device bytes per quad block
+    extern __shared__ __align__(16) unsigned char stage_lds[];  // [2][STAGE]
+    const int tid = threadIdx.x, lane = tid & 63, i = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tx, ty;
+    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + BN - 1) / BN, (p.M + BM - 1) / BM, tx, ty);
+    const int m0 = ty * BM, n0 = p.col_begin + tx * BN;
+    const int B = p.B, G = p.G;
+    const int stages = (B + KB - 1) / KB;
+    const int last_col = p.col_end - 1;
+
+    // The direct loads of stage s into buffer `buf`, spread over the four waves (uniform branches).
+    // (Stage offsets are taken out of the lambda: a static member of the tile type used inside it
+    // drops the kernel's host-side launch stub.)
+    unsigned char *const w_lds = stage_lds + T::A_BYTES, *const as_lds = w_lds + T::W_BYTES, *const ws_lds = as_lds + T::AS_BYTES;
+    constexpr int kStage = T::STAGE, kALoads = T::A_LOADS, kWLoads = T::W_LOADS, kASLanes = T::AS_LANES, kWSLanes = T::WS_LANES;
+    auto issue = [&](int s, int buf) {
+        unsigned char *base = stage_lds + buf * kStage;
+        const int boff = buf * kStage;
+        const int g0 = s * KB;
+        for (int k = wave; k < kALoads; k += 4) {
+            constexpr int per = BM / 32;  // loads per block
+            const int kb = k / per, r = (k - kb * per) * 32 + (lane >> 1);
+            const int row = min(m0 + r, p.M - 1), blk = min(g0 + kb, B - 1);
+            // row r's two 16-byte halves sit swapped when bit 2 of r is set: a wave's reads of
+            // eight consecutive rows then touch 32 distinct banks
+            __builtin_amdgcn_global_load_lds(p.q + size_t(row) * p.K + blk * 32 + ((lane ^ (lane >> 3)) & 1) * 16,
+                                             base + k * 1024, 16, 0, 0);
+        }
+        for (int k = wave; k < kWLoads; k += 4) {
+            const int8_t *src;
+            if (FMT == 8) {
+                constexpr int per = BN / 32;
+                const int kb = k / per, c = min(n0 + (k - kb * per) * 32 + (lane >> 1), last_col), blk = min(g0 + kb, B - 1);
+                src = p.codes + size_t(c >> 2) * B * QB + size_t(blk) * QB + (c & 3) * 32 + ((lane ^ (lane >> 3)) & 1) * 16;
+            } else {
+                constexpr int per = BN / 64;
+                const int kb = k / per, c = min(n0 + (k - kb * per) * 64 + lane, last_col), blk = min(g0 + kb, B - 1);
+                src = p.codes + size_t(c >> 2) * B * QB + size_t(blk) * QB + (c & 3) * 16;
+            }
+            __builtin_amdgcn_global_load_lds(src, w_lds + boff + k * 1024, 16, 0, 0);
+        }
+        if (wave == 2 && lane < kASLanes) {
+            // four rows' scales of one block per lane: as_t [G][Mpad], Mpad a multiple of BM
+            const int kb = lane / (BM / 4), r = (lane - kb * (BM / 4)) * 4, blk = min(g0 + kb, B - 1);
+            __builtin_amdgcn_global_load_lds(p.as_t + size_t(blk) * p.Mpad + m0 + r, as_lds + boff, 16, 0, 0);
+        }
+        if (wave == 3 && lane < kWSLanes) {
+            // the four lanes' scales of one quad and block per lane
+            const int kb = lane / (BN / 4), qd = lane - kb * (BN / 4), blk = min(g0 + kb, B - 1);
+            const int q = min((n0 >> 2) + qd, last_col >> 2);
+            __builtin_amdgcn_global_load_lds(p.wscales + (size_t(q) * G + blk) * 4, ws_lds + boff, 16, 0, 0);
+        }
+    };
+
+    float acc[WM][WN][16];
+#pragma unroll
+    for (int a = 0; a < WM; a++)
+#pragma unroll
+        for (int b = 0; b < WN; b++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+    const int wr0 = (wave >> 1) * 32 * WM, wc0 = (wave & 1) * 32 * WN;
+    const int half = 16 * (h ^ ((i >> 2) & 1));  // the staged half of this lane's row (see issue)
+
+    issue(0, 0);
+    for (int s = 0; s < stages; s++) {
+        const int buf = s & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of stage s
+        __syncthreads();  // every wave's loads of stage s; every wave done with stage s - 1
+        if (s + 1 < stages) issue(s + 1, buf ^ 1);
+        const unsigned char *base = stage_lds + buf * kStage;
+        const int8_t *As = reinterpret_cast<const int8_t *>(base);
+        const int8_t *Ws = As + T::A_BYTES;
+        const float *ASs = reinterpret_cast<const float *>(Ws + T::W_BYTES);
+        const float *WSs = ASs + KB * BM;
+        // Per pair of blocks, the scale products fl(ws·as) come from one f32 MFMA outer product
+        // per sub-tile (v_mfma_f32_32x32x1_2b: lanes 0..31 give the first block's row and column
+        // scales, lanes 32..63 the second's; exactly the VALU's rounded products, subnormals
+        // included), in the layout of the int8 products: one scale read per lane, not sixteen.
+#pragma unroll
+        for (int pr = 0; pr < KB / 2; pr++) {
+            const int kb0 = 2 * pr;
+            if (s * KB + kb0 >= B) break;  // uniform
+            const bool second = s * KB + kb0 + 1 < B;
+            float asv[WM], wsv[WN];
+            v4i a[2][WM], w[2][WN];
+#pragma unroll
+            for (int rt = 0; rt < WM; rt++) asv[rt] = ASs[(kb0 + h) * BM + wr0 + rt * 32 + i];
+#pragma unroll
+            for (int ct = 0; ct < WN; ct++) wsv[ct] = WSs[(kb0 + h) * BN + wc0 + ct * 32 + i];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++) {
+                const int kb = kb0 + k2;
+#pragma unroll
+                for (int rt = 0; rt < WM; rt++)
+                    a[k2][rt] = *reinterpret_cast<const v4i *>(As + (kb * BM + wr0 + rt * 32 + i) * 32 + half);
+#pragma unroll
+                for (int ct = 0; ct < WN; ct++) {
+                    const int c = wc0 + ct * 32 + i;
+                    if (FMT == 8) {
+                        w[k2][ct] = *reinterpret_cast<const v4i *>(Ws + (kb * BN + c) * RB + half);
+                    } else {
+                        const v4i x = *reinterpret_cast<const v4i *>(Ws + (kb * BN + c) * RB);
+                        const int sh = h * 4;
+                        w[k2][ct] = v4i{nibbles_signed(x.x >> sh), nibbles_signed(x.y >> sh), nibbles_signed(x.z >> sh),
+                                        nibbles_signed(x.w >> sh)};
+                    }
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < WM; rt++)
+#pragma unroll
+                for (int ct = 0; ct < WN; ct++) {
+                    const v32f zero32 = {0};
+                    const v32f pp = __builtin_amdgcn_mfma_f32_32x32x1f32(asv[rt], wsv[ct], zero32, 0, 0, 0);
+#pragma unroll
+                    for (int k2 = 0; k2 < 2; k2++) {
+                        if (k2 == 1 && !second) break;
+                        const v16i zero = {0};
+                        const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[k2][rt], w[k2][ct], zero, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 16; v++)
+                            acc[rt][ct][v] = FUSED ? __builtin_fmaf(float(d[v]), pp[16 * k2 + v], acc[rt][ct][v])
+                                                   : acc[rt][ct][v] + float(d[v]) * pp[16 * k2 + v];
+                    }
+                }
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < WM; rt++)
+#pragma unroll
+        for (int ct = 0; ct < WN; ct++) {
+            const int n = n0 + wc0 + ct * 32 + i;
+            if (n > last_col) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int r = m0 + wr0 + rt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (r >= p.M) continue;
+                float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+                float y = acc[rt][ct][v];
+                if (p.bias && n < p.n_rows) y = y + p.bias[n];
+                *o = p.accumulate ? *o + y : y;
+            }
+        }
+}
+
 // as [M][G] -> as_t [G][Mpad] (zeros past M).
 __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int G, int Mpad, float *__restrict__ as_t)
 {
@@ -714,6 +896,25 @@ template <int FMT>
 int launch_tiles(const GemmParams &p, bool dots, bool lds, bool fused, hipStream_t s)
 {
     return fused && !dots ? launch_tiles_as<FMT, true>(p, dots, lds, s) : launch_tiles_as<FMT, false>(p, dots, lds, s);
+}
+
+template <int FMT, int WM, int WN>
+int launch_lds_as(const GemmParams &p, bool fused, hipStream_t s)
+{
+    using T = LdsTile<FMT, WM, WN>;
+    const long groups = long((p.col_end - p.col_begin + T::BN - 1) / T::BN) * ((p.M + T::BM - 1) / T::BM);
+    const size_t smem = 2 * size_t(T::STAGE);
+    if (fused) gemm_lds_kernel<FMT, WM, WN, true><<<unsigned(groups), 256, smem, s>>>(p);
+    else gemm_lds_kernel<FMT, WM, WN, false><<<unsigned(groups), 256, smem, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+// tiles: 10·WM + WN (workgroup tiles of 64·WM rows x 64·WN columns)
+template <int FMT>
+int launch_lds(const GemmParams &p, int tiles, bool fused, hipStream_t s)
+{
+    return tiles == 21 ? launch_lds_as<FMT, 2, 1>(p, fused, s) : launch_lds_as<FMT, 1, 1>(p, fused, s);
 }
 
 // T2b128 (ternary levels, one scale per 128 inputs: matmul.rs:461-469, quant.rs:168-177): one
@@ -790,32 +991,70 @@ hipError_t workspace_alloc(void **ptr, size_t bytes, hipStream_t s)
     return hipMallocFromPoolAsync(ptr, bytes, pool, s);
 }
 
-// The scratch of a product: the levels, scales and corrections of f32 rows it quantizes first, and
-// the block-major copy of the activation scales when a tile's do not fit in LDS. Each part starts
-// on a 256-byte boundary.
+// Which kernel a batched product runs, and the scratch it needs: the levels, scales and
+// corrections of f32 rows it quantizes first, and the block-major copy of the activation scales
+// (as_t [G][Mpad]) when the kernel reads that rather than staging a tile's scales itself. Each
+// part starts on a 256-byte boundary.
 struct ScratchPlan {
     size_t q_bytes, s_bytes, t_bytes;
-    bool lds;
+    bool lds;    // the register-ring kernels stage the tile's scales in LDS
+    int tiles;   // 0: the register-ring kernels; else the LDS-staged kernel, 10·WM + WN
+    int Mpad;    // rows of as_t
     size_t total() const { return q_bytes + 2 * s_bytes + t_bytes; }
 };
+
+// Workgroups of the LDS-staged kernel at a tile shape.
+static long lds_groups(const ProductArgs &a, int wm, int wn)
+{
+    const long cols = long(a.quad_end - a.quad_begin) * 4, rows = long(a.rows);
+    return ((cols + 64 * wn - 1) / (64 * wn)) * ((rows + 64 * wm - 1) / (64 * wm));
+}
+
+// The kernel of a batched product: 0 for the register-ring kernels, else the LDS-staged kernel's
+// tile shape. FG_GEMM_TILE (0, 11 or 21) overrides the choice, for tests and measurements.
+static int choose_tiles(const ProductArgs &a)
+{
+    const fg_table *t = a.t;
+    if (a.dots || t->dtype == FG_T2B128 || a.rows <= 16) return 0;
+    if (const char *env = getenv("FG_GEMM_TILE")) {
+        const int v = atoi(env);
+        if (v == 0 || v == 11 || v == 21) return v;
+    }
+    const long ncols = long(a.quad_end - a.quad_begin) * 4;
+    const long narrow = ((ncols + 31) / 32) * ((long(a.rows) + 31) / 32);
+    const size_t split_smem = size_t(t->groups) * 32 * 4 + 2 * 4 * 4 * 64 * 16;
+    // few 32 x 32 tiles: four waves per tile over alternate groups (gemm_split_kernel), or for the
+    // fused scaling one wave per tile (gemm_kernel)
+    if (narrow < 2048 && (a.fused || (t->groups % 4 == 0 && split_smem <= 64 * 1024))) return 0;
+    // 128 x 64 workgroup tiles while they still make two rounds of workgroups (four per CU),
+    // else 64 x 64 (measured on the DiT block's 4096-row products and 512-row prefill)
+    return lds_groups(a, 2, 1) >= 1536 ? 21 : 11;
+}
 
 ScratchPlan plan_scratch(const ProductArgs &a)
 {
     const fg_table *t = a.t;
     const size_t M = a.rows, K = t->cols, G = t->groups;
-    const size_t Mpad = (M + 63) / 64 * 64;
     ScratchPlan pl{};
     pl.q_bytes = a.x ? (M * K + 255) / 256 * 256 : 0;
     pl.s_bytes = a.x ? (M * G * 4 + 255) / 256 * 256 : 0;
+    pl.Mpad = int((M + 63) / 64 * 64);
     if (t->dtype == FG_T2B128) {
         pl.lds = true;
+        return pl;
+    }
+    pl.tiles = choose_tiles(a);
+    if (pl.tiles) {
+        // the staged kernel reads whole tiles of as_t: rows padded to 128
+        pl.Mpad = int((M + 127) / 128 * 128);
+        pl.t_bytes = G * size_t(pl.Mpad) * 4;
         return pl;
     }
     // The activation scales go to LDS per tile when a tile's fit in 64 KiB and their rows are
     // whole float4s; otherwise the kernel reads a block-major copy.
     const bool dots = a.dots != nullptr;
     pl.lds = !dots && G * 32 * 4 <= 64 * 1024 && G % 4 == 0 && (a.x || (reinterpret_cast<uintptr_t>(a.as) & 15) == 0);
-    pl.t_bytes = (pl.lds || dots) ? 0 : G * Mpad * 4;
+    pl.t_bytes = (pl.lds || dots) ? 0 : G * size_t(pl.Mpad) * 4;
     return pl;
 }
 
@@ -877,10 +1116,10 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
     const fg_table *t = a.t;
     if (t->dtype == FG_T2B128) return launch_t2(a, s);
     const int M = int(a.rows), K = int(t->cols), G = int(t->groups);
-    const int Mpad = (M + 63) / 64 * 64;
     const bool dots = a.dots != nullptr;
     // Workspace: levels, scales and corrections (when the input is f32), block-major scales.
     const ScratchPlan pl = plan_scratch(a);
+    const int Mpad = pl.Mpad;
     const bool lds = pl.lds;
     const size_t q_bytes = pl.q_bytes, s_bytes = pl.s_bytes, t_bytes = pl.t_bytes;
     void *ws = nullptr;
@@ -925,7 +1164,10 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.accumulate = a.accumulate;
         p.dots = a.dots;
         p.dots_cols = p.col_end - p.col_begin;
-        rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, lds, a.fused != 0, s) : launch_tiles<8>(p, dots, lds, a.fused != 0, s);
+        if (pl.tiles)
+            rc = t->dtype == FG_Q4B32 ? launch_lds<4>(p, pl.tiles, a.fused != 0, s) : launch_lds<8>(p, pl.tiles, a.fused != 0, s);
+        else
+            rc = t->dtype == FG_Q4B32 ? launch_tiles<4>(p, dots, lds, a.fused != 0, s) : launch_tiles<8>(p, dots, lds, a.fused != 0, s);
     }
     if (owned) {
         hipError_t e = hipFreeAsync(ws, s);

@@ -11,11 +11,15 @@ algorithmic bytes (weight codes + scales + int8 activations with scales and corr
 outputs) over the kernel's duration, measured with HIP events on the launch stream.
 
 `cpu_baseline` is the oracle (a C restatement of the reference's scalar x86-64 path, column-split
-over threads like the reference's team) timed on this host on a bounded number of decode steps.
+over threads like the reference's team) timed on this host: the decode step at the reference CLI's
+default team of min(8, cores - 2) threads, one warm-up then the mean over a bounded number of steps,
+the steady-state best of five, and the same on every core; the host's CPU model and count.
 
-Extra fields: the single 4864 x 896 matvec (resident and streamed over > 256 MiB of weights), the
-batched GEMMs (512 x 896 -> 9728, 512 x 4864 -> 896, DiT 4096-row shapes) and the packed-int4
-14336 x 4096 product (rows 1 and 16).
+Extra fields: the single 4864 x 896 matvec (resident; streamed over 64 copies, one launch each;
+all 64 copies as one 311296 x 896 table in one launch), the batched GEMMs (512 x 896 -> 9728,
+512 x 4864 -> 896, DiT 4096-row shapes), the packed-int4 14336 x 4096 product (rows 1 and 16)
+and the int8 attention at the DiT shape. Every product carries its own CPU baseline (the oracle's
+quantization and product, same protocol; the 4096-row shapes on a sample of their rows).
 """
 
 import argparse
@@ -51,6 +55,81 @@ def measured_traffic():
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def host_cpu():
+    """The host's CPU model, logical CPU count and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = nproc
+    return model, nproc, usable
+
+
+def cpu_thread_counts():
+    """The reference CLI's default team, min(8, cores - 2) (crates/harness/src/lib.rs:36-44), and
+    every core this process may use."""
+    _, _, usable = host_cpu()
+    return max(1, min(8, usable - 2)), usable
+
+
+def cpu_protocol(call, calls=3):
+    """Milliseconds per call two ways: one warm-up call then the mean of `calls` calls
+    (crates/harness/src/bench.rs:8-17), and the steady state of tools/kernel-harness/bench.mjs:29-40
+    (iterations doubling until a run takes at least 80 ms, then the best of five runs)."""
+    call()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        call()
+    mean_ms = (time.perf_counter() - t0) * 1e3 / calls
+    iters = 1
+    while True:
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            call()
+        if time.perf_counter() - t0 >= 0.08:
+            break
+        iters *= 2
+    best = float("inf")
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            call()
+        best = min(best, time.perf_counter() - t0)
+    return mean_ms, best * 1e3 / iters
+
+
+def cpu_product_baseline(np, dtype, n, k, table_bytes, x, rate, unit, sample):
+    """The oracle's product (quantize_rows, then the column- or row-split product of the
+    reference's scalar path) on this host at the reference's default team size and on every core;
+    `rate(ms)` turns milliseconds per call into the workload's figure."""
+    from oracle import oracle as O
+    rows = x.shape[0]
+    default, every = cpu_thread_counts()
+    model, nproc, _ = host_cpu()
+
+    def run(threads):
+        def call():
+            q, sc, co = O.quantize_rows(x.reshape(-1), dtype)
+            O.matmul_threaded(dtype, n, k, table_bytes, q, sc, co, rows, threads=threads)
+        mean_ms, best_ms = cpu_protocol(call)
+        return {"value": float(f"{rate(best_ms):.4g}"), "mean_ms": round(mean_ms, 3), "best_of_5_ms": round(best_ms, 3)}
+
+    line = {"unit": unit, "cores": default, "kind": "port", "sample": sample, "cpu": model, "nproc": nproc,
+            "value_from": "best of 5 (mean of 3 after one warm-up also given)"}
+    line.update(run(default))
+    line["all_cores"] = dict(run(every), cores=every)
+    return line
 
 
 def synthetic_table(np, dtype, rows, cols, rng):
@@ -225,11 +304,13 @@ def time_matvecs(fk, torch, np, shape, host):
     return total_bytes, total_ms, len(launches), detail
 
 
-def cpu_baseline(np, shape, host, budget_s=12.0):
-    """The oracle's decode step on this host's cores (threads as the reference's CLI defaults:
-    min(8, cores - 2)), repeated until about `budget_s` seconds of CPU work."""
+def cpu_baseline(np, shape, host, budget_s=10.0):
+    """The oracle's decode step on this host (a C restatement of the reference's scalar x86-64
+    path, its products column-split over a team of threads like the reference's): at the
+    reference CLI's default team, min(8, cores - 2) threads, one warm-up step then the mean over
+    as many steps as fit in about `budget_s` seconds (crates/harness/src/bench.rs:8-17), and the
+    steady-state best of five runs (tools/kernel-harness/bench.mjs:29-40); the same on every core."""
     from oracle import oracle as O
-    import torch
     layers = []
     for d in host["layers"]:
         layers.append({k: d[k].reference_bytes() for k in ("qkv", "o", "gate", "up", "down")}
@@ -239,27 +320,50 @@ def cpu_baseline(np, shape, host, budget_s=12.0):
                       rope_base=shape.rope_base, eps=shape.eps, dtype=O.Q7B32)
     model = O.Qwen2(sh, layers, host["final"].cpu().numpy(), host["table_bytes"])
     kc, vc = host["kc"].cpu().numpy(), host["vc"].cpu().numpy()
-    cores = os.cpu_count() or 1
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        pass
-    threads = max(1, min(8, cores - 2))
-    model.step(kc, vc, 1234, 511, threads=threads)  # warm-up (harness/src/bench.rs:8-17)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        model.step(kc, vc, 1234, 511, threads=threads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 200:
-            break
-    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps at position 511 (full 24-layer step with logits), {threads} threads, "
-                      f"{el:.1f} s; C restatement of the reference scalar path"}
+    default, every = cpu_thread_counts()
+    cpu_model, nproc, _ = host_cpu()
+
+    def measure(threads, budget):
+        step = lambda: model.step(kc, vc, 1234, 511, threads=threads)  # noqa: E731
+        step()  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while True:
+            step()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget or n >= 200:
+                break
+        iters = 1
+        while True:
+            t1 = time.perf_counter()
+            for _ in range(iters):
+                step()
+            if time.perf_counter() - t1 >= 0.08:
+                break
+            iters *= 2
+        best = min(timed(step, iters) for _ in range(5)) / iters
+        return n, el, {"value": round(n / el, 3), "mean_ms_per_step": round(el * 1e3 / n, 3),
+                       "best_of_5_ms_per_step": round(best * 1e3, 3)}
+
+    n, el, line = measure(default, budget_s)
+    _, _, every_line = measure(every, budget_s / 2)
+    line.update({"unit": "tokens/s", "cores": default, "kind": "port", "cpu": cpu_model, "nproc": nproc,
+                 "sample": f"{n} decode steps at position 511 (the full 24-layer step with logits) after one warm-up, "
+                           f"{default} threads, {el:.1f} s; value = the mean; C restatement of the reference scalar path",
+                 "all_cores": dict(every_line, cores=every)})
+    return line
 
 
-def extras(fk, torch, np):
-    """The other workloads: single matvec (resident and streamed), GEMMs, packed int4."""
+def timed(call, iters):
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        call()
+    return time.perf_counter() - t0
+
+
+def extras(fk, torch, np, with_cpu=True):
+    """The other workloads: single matvec (resident, streamed over 64 launches, and in one launch
+    over all 64 copies), GEMMs, packed int4, int8 attention; each product with its CPU baseline."""
     timer = Timer(torch)
     rng = np.random.default_rng(0)
     res = {}
@@ -268,65 +372,95 @@ def extras(fk, torch, np):
         n, k = 4864, 896
         data = synthetic_table(np, dtype, n, k, rng)
         t = fk.Table(fk.Tensor(dtype, [n, k], data))
-        x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).cuda()
+        xh = rng.standard_normal(k).astype(np.float32)
+        x = torch.from_numpy(xh).cuda()
         out = torch.empty((1, n), dtype=torch.float32, device="cuda")
         m = t.matrix()
         inp_x = fk.Input(f32=x)
         ms = timer(lambda: fk.matmul(m, inp_x, range(0, n), out=out), 200, graph=True)
         b = matvec_bytes(n, k, dtype, f32_input=True)
-        entry = {"resident_us": round(ms * 1e3, 3), "resident_GB_s": round(b / ms / 1e6, 1)}
+        entry = {"resident_us": round(ms * 1e3, 3), "resident_GB_s": round(b / ms / 1e6, 1), "bytes": b}
         if dtype == Q8B32:
-            # streamed: 64 distinct copies (> 256 MiB Infinity Cache) read in turn
+            # streamed: 64 distinct copies (> 256 MiB Infinity Cache) read in turn, one launch each
             copies = [fk.Table.from_device_bytes(dtype, n, k, torch.from_numpy(data).cuda()) for _ in range(64)]
-            ms_list = []
             mats = [c.matrix() for c in copies]
 
             def sweep():
                 for mm in mats:
-                    fk.matmul(mm, fk.Input(f32=x), range(0, n), out=out)
+                    fk.matmul(mm, inp_x, range(0, n), out=out)
             ms = timer(sweep, 5, graph=True) / len(mats)
             entry.update({"streamed_us": round(ms * 1e3, 3), "streamed_GB_s": round(b / ms / 1e6, 1),
                           "streamed_bytes": 64 * len(data)})
-            del copies, mats, ms_list
+            del copies, mats
+            # sustained: the 64 copies' rows as one 311296 x 896 table (314 MB, past the 256 MiB
+            # Infinity Cache), streamed by one launch
+            big_rows = 64 * n
+            big = fk.Table(fk.Tensor(dtype, [big_rows, k], synthetic_table(np, dtype, big_rows, k, rng)))
+            big_out = torch.empty((1, big_rows), dtype=torch.float32, device="cuda")
+            bm = big.matrix()
+            ms = timer(lambda: fk.matmul(bm, inp_x, range(0, big_rows), out=big_out), 20, graph=True)
+            bb = matvec_bytes(big_rows, k, dtype, f32_input=True)
+            entry.update({"one_launch_311296x896_us": round(ms * 1e3, 3), "one_launch_GB_s": round(bb / ms / 1e6, 1),
+                          "one_launch_frac_hbm": round(bb / ms / 1e6 / HBM_PEAK_GBS, 4), "one_launch_bytes": bb})
+            del big, bm, big_out
+        if with_cpu:
+            entry["cpu_baseline"] = cpu_product_baseline(
+                np, dtype, n, k, data, xh.reshape(1, k), lambda ms_: b / ms_ / 1e6, "GB/s",
+                "the whole 4864 x 896 product, f32 row quantized first")
         res[f"matvec_4864x896_{name}"] = entry
-    # 2. GEMMs (f32 activations quantized first; Q8b32 weights)
-    for label, (rows, k, n, outl, sigma) in {"gemm_512x896x9728": (512, 896, 9728, 0.0, 1.0),
-                                              "gemm_512x4864x896": (512, 4864, 896, 0.0, 1.0),
-                                              "dit_qkv_4096x1152x3456": (4096, 1152, 3456, 0.01, 2.0 ** 0.5),
-                                              "dit_up_4096x1152x4608": (4096, 1152, 4608, 0.01, 2.0 ** 0.5),
-                                              "dit_down_4096x4608x1152": (4096, 4608, 1152, 0.01, 2.0 ** 0.5)}.items():
-        t = fk.Table(fk.Tensor(Q8B32, [n, k], synthetic_table(np, Q8B32, n, k, rng)))
+    # 2. GEMMs (Q8b32 weights); the CPU baseline on a sample of rows for the 4096-row shapes
+    for label, (rows, k, n, outl, sigma, cpu_rows) in {
+            "gemm_512x896x9728": (512, 896, 9728, 0.0, 1.0, 512),
+            "gemm_512x4864x896": (512, 4864, 896, 0.0, 1.0, 512),
+            "dit_qkv_4096x1152x3456": (4096, 1152, 3456, 0.01, 2.0 ** 0.5, 256),
+            "dit_up_4096x1152x4608": (4096, 1152, 4608, 0.01, 2.0 ** 0.5, 256),
+            "dit_down_4096x4608x1152": (4096, 4608, 1152, 0.01, 2.0 ** 0.5, 256)}.items():
+        data = synthetic_table(np, Q8B32, n, k, rng)
+        t = fk.Table(fk.Tensor(Q8B32, [n, k], data))
         xh = (rng.standard_normal((rows, k)) * sigma).astype(np.float32)
         if outl:
             xh[rng.random((rows, k)) < outl] *= 20
         x = torch.from_numpy(xh).cuda()
         m = t.matrix()
         out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
-        ms_f32 = timer(lambda: fk.matmul(m, fk.Input(f32=x.view(-1)), range(0, n), out=out), 10)
+        ms_f32 = timer(lambda: fk.matmul(m, fk.Input(f32=x.view(-1)), range(0, n), out=out), 10, graph=True)
         qr = fk.QuantizedRows()
         inp = qr.input(m, x.view(-1))
         ms_q = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 10, graph=True)
         # the NEON backend's arithmetic (one fused multiply-add per group scaling), its own bits
         ms_fused = timer(lambda: fk.matmul(m, inp, range(0, n), out=out, fused=True), 10, graph=True)
         ops = 2.0 * rows * n * k
-        res[label] = {"with_quantization_launched_us": round(ms_f32 * 1e3, 2), "prequantized_us": round(ms_q * 1e3, 2),
-                      "TOPS": round(ops / ms_q / 1e9, 1), "frac_int8_peak": round(ops / ms_q / 1e9 / INT8_PEAK_TOPS, 4),
-                      "fused_scale_us": round(ms_fused * 1e3, 2), "fused_scale_TOPS": round(ops / ms_fused / 1e9, 1),
-                      "fused_scale_frac_int8_peak": round(ops / ms_fused / 1e9 / INT8_PEAK_TOPS, 4)}
+        entry = {"with_quantization_us": round(ms_f32 * 1e3, 2), "with_quantization_TOPS": round(ops / ms_f32 / 1e9, 1),
+                 "prequantized_us": round(ms_q * 1e3, 2),
+                 "TOPS": round(ops / ms_q / 1e9, 1), "frac_int8_peak": round(ops / ms_q / 1e9 / INT8_PEAK_TOPS, 4),
+                 "fused_scale_us": round(ms_fused * 1e3, 2), "fused_scale_TOPS": round(ops / ms_fused / 1e9, 1),
+                 "fused_scale_frac_int8_peak": round(ops / ms_fused / 1e9 / INT8_PEAK_TOPS, 4)}
+        if with_cpu:
+            cpu_ops = 2.0 * cpu_rows * n * k
+            entry["cpu_baseline"] = cpu_product_baseline(
+                np, Q8B32, n, k, data, xh[:cpu_rows], lambda ms_: cpu_ops / ms_ / 1e9, "TOPS",
+                f"the first {cpu_rows} of {rows} rows (rows are independent), f32 rows quantized first")
+        res[label] = entry
     # 3. packed int4 14336 x 4096, rows 1 and 16
     n, k = 14336, 4096
-    t = fk.Table(fk.Tensor(Q4B32, [n, k], synthetic_table(np, Q4B32, n, k, rng)))
+    data = synthetic_table(np, Q4B32, n, k, rng)
+    t = fk.Table(fk.Tensor(Q4B32, [n, k], data))
     m = t.matrix()
     for rows in (1, 16):
-        x = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float32)).cuda()
+        xh = rng.standard_normal((rows, k)).astype(np.float32)
+        x = torch.from_numpy(xh).cuda()
         inp = fk.QuantizedRows().input(m, x.view(-1))
         out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
         ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 50, graph=True)
         b = n * k // 2 + n * k // 32 * 4 + rows * (k + k // 32 * 8) + rows * n * 4
-        res[f"int4_14336x4096_rows{rows}"] = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1)}
+        entry = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
+                 "bytes": b}
+        if with_cpu:
+            entry["cpu_baseline"] = cpu_product_baseline(np, Q4B32, n, k, data, xh, lambda ms_: b / ms_ / 1e6, "GB/s",
+                                                         f"the whole product, {rows} f32 row(s) quantized first")
+        res[f"int4_14336x4096_rows{rows}"] = entry
     # 4. int8 attention (attention::attend) at the DiT block's shape: 4096 tokens, 16 heads of 72
-    #    read by stride and offset from one fused qkv row, exp_fast; each call quantizes the keys
-    #    and values, allocates its scratch and waits for its stream
+    #    read by stride and offset from one fused qkv row, exp_fast
     tokens, heads, hd = 4096, 16, 72
     row = 3 * heads * hd
     qkv = torch.from_numpy(rng.standard_normal((tokens, row)).astype(np.float32)).cuda()
@@ -382,7 +516,7 @@ def main():
         del ex_model
     if not args.no_extras:
         log("extra workloads...")
-        other.update(extras(fk, torch, np))
+        other.update(extras(fk, torch, np, with_cpu=not args.no_cpu))
     cpu = None
     if not args.no_cpu:
         log("cpu baseline...")

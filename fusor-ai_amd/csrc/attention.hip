@@ -18,6 +18,7 @@
 #include "common.h"
 #include "proj.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace fg {
@@ -25,6 +26,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxRowBytes = 64 * 1024;  // one padded score row in LDS: at most 16384 keys
+constexpr int kMaxHeadDim = 1024;
 
 size_t pad32(size_t n) { return (n + 31) / 32 * 32; }
 
@@ -43,86 +45,218 @@ __device__ __forceinline__ float ref_exp_fast(float x)
     return poly * __int_as_float((int(n) + 127) << 23);
 }
 
-// mean[(image · kv_heads + kh) · hd + d] = (Σ over the image's keys in order of key[d]) / keys,
-// one thread per (image, key head, channel), every key head of the call in one launch; each
-// thread issues 32 keys' loads before it adds them, in order
-__global__ void key_mean_kernel(const float *__restrict__ key, size_t stride, size_t offset, int images, int kv_heads,
-                                int keys, int hd, float *__restrict__ mean)
+// keyT[(t · hd + d) · kpad + k] = key[k][d] of table t = image · kv_heads + kh: the keys of every
+// (image, key head) with channels as rows, through 64 x 64 tiles in LDS (both sides coalesced).
+__global__ __launch_bounds__(256) void key_transpose_kernel(const float *__restrict__ key, size_t stride, size_t offset,
+                                                            int kv_heads, int keys, int hd, int kpad,
+                                                            float *__restrict__ keyT)
 {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(images) * kv_heads * hd) return;
-    const int d = int(i % hd);
-    const size_t ih = i / hd;
-    const int kh = int(ih % kv_heads);
-    const size_t image = ih / kv_heads;
-    const float *base = key + image * size_t(keys) * stride + offset + size_t(kh) * hd + d;
-    float s = 0.0f;
-    for (int k0 = 0; k0 < keys; k0 += 32) {
-        float v[32];
-#pragma unroll
-        for (int u = 0; u < 32; u++) v[u] = base[size_t(min(k0 + u, keys - 1)) * stride];
-#pragma unroll
-        for (int u = 0; u < 32; u++)
-            if (k0 + u < keys) s = s + v[u];
+    __shared__ float tile[64][65];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int k0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+    const size_t t = blockIdx.z, image = t / kv_heads, kh = t % kv_heads;
+    const float *src = key + image * size_t(keys) * stride + offset + kh * size_t(hd);
+    for (int kk = ty; kk < 64; kk += 4) {
+        const int k = k0 + kk, d = d0 + tx;
+        if (k < keys && d < hd) tile[kk][tx] = src[size_t(k) * stride + d];
     }
-    mean[i] = s / float(keys);
+    __syncthreads();
+    for (int dd = ty; dd < 64; dd += 4) {
+        const int d = d0 + dd, k = k0 + tx;
+        if (k < keys && d < hd) keyT[(t * hd + d) * size_t(kpad) + k] = tile[tx][dd];
+    }
 }
 
-// rows[k][d] = key[k][d] − mean[d] for d < hd, zeros to the padded width pd
-__global__ void key_rows_kernel(const float *__restrict__ key, size_t stride, size_t base, int keys, int hd, int pd,
-                                const float *__restrict__ mean, float *__restrict__ rows)
+// mean[t · hd + d] = (Σ over the keys in order of key[k][d]) / keys, from the transposed keys:
+// one wave per (table, channel) brings the channel's keys into LDS, sixteen coalesced loads of
+// 256 keys in flight, then its first lane adds them in key order (the reference's sequential sum).
+__global__ __launch_bounds__(64) void key_mean_kernel(const float *__restrict__ keyT, int keys, int kpad,
+                                                      float *__restrict__ mean)
 {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(keys) * pd) return;
-    const int k = int(i / pd), d = int(i % pd);
-    rows[i] = d < hd ? key[base + size_t(k) * stride + d] - mean[d] : 0.0f;
+    extern __shared__ __align__(16) float column[];  // [keys rounded up to 4096]
+    const int lane = threadIdx.x;
+    const size_t id = blockIdx.x;
+    const v4f *src = reinterpret_cast<const v4f *>(keyT + id * size_t(kpad));
+    v4f *col4 = reinterpret_cast<v4f *>(column);
+    const int n4 = kpad / 4;
+    for (int s0 = 0; s0 < n4; s0 += 1024) {
+        v4f v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = src[min(s0 + 64 * u + lane, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; u++) col4[s0 + 64 * u + lane] = v[u];
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float s = 0.0f;
+        int k = 0;
+        for (; k + 16 <= keys; k += 16) {
+            v4f x[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) x[u] = col4[k / 4 + u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                s = s + x[u].x;
+                s = s + x[u].y;
+                s = s + x[u].z;
+                s = s + x[u].w;
+            }
+        }
+        for (; k < keys; k++) s = s + column[k];
+        mean[id] = s / float(keys);
+    }
 }
 
-// rows[d][k] = value[k][d] for k < keys, zeros to the padded width pk (Scratch::transpose)
-__global__ void value_rows_kernel(const float *__restrict__ value, size_t stride, size_t base, int keys, int hd, int pk,
-                                  float *__restrict__ rows)
+// The cleared row-block of a run-time Q7b32 matrix (QuantizedMatrix::extend's padding rows):
+// zero codes (device levels −64) and a zero scale.
+__device__ __forceinline__ void clear_block(int8_t *codes32, float *scale)
 {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(hd) * pk) return;
-    const int d = int(i / pk), k = int(i % pk);
-    rows[i] = k < keys ? value[base + size_t(k) * stride + d] : 0.0f;
+    int4 *dst = reinterpret_cast<int4 *>(codes32);
+    const int v = int(0xC0C0C0C0u);
+    dst[0] = make_int4(v, v, v, v);
+    dst[1] = make_int4(v, v, v, v);
+    *scale = 0.0f;
 }
 
-// rows[r][d] = query[r][d] for d < hd, zeros to pd
-__global__ void query_rows_kernel(const float *__restrict__ query, size_t stride, size_t base, int queries, int hd,
-                                  int pd, float *__restrict__ rows)
+// Scratch::quantize's key matrices (attention.rs:100-118) for every (image, key head) at once:
+// row k of table t is key[k] − mean over the channels, zeros to the padded width; rows past the
+// keys to the quad are cleared. One thread per (table, row, block).
+__global__ void key_table_kernel(const float *__restrict__ key, size_t stride, size_t offset, int kv_heads, int keys,
+                                 int hd, int rows4, int blocks, const float *__restrict__ mean, int8_t *__restrict__ codes,
+                                 float *__restrict__ scales, size_t tables)
 {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(queries) * pd) return;
-    const int r = int(i / pd), d = int(i % pd);
-    rows[i] = d < hd ? query[base + size_t(r) * stride + d] : 0.0f;
+    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= tables * rows4 * blocks) return;
+    const int b = int(id % blocks), row = int(id / blocks % rows4);
+    const size_t t = id / (size_t(blocks) * rows4);
+    const size_t tb = (t * (rows4 / 4) + row / 4) * blocks + b;  // quad block of the tables' run
+    int8_t *dst = codes + tb * 128 + (row % 4) * 32;
+    float *scale = scales + tb * 4 + row % 4;
+    if (row >= keys) {
+        clear_block(dst, scale);
+        return;
+    }
+    const size_t image = t / kv_heads, kh = t % kv_heads;
+    const float *src = key + (image * size_t(keys) + row) * stride + offset + kh * size_t(hd);
+    const float *mu = mean + t * hd;
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int d = 32 * b + i;
+        x[i] = d < hd ? src[d] - mu[d] : 0.0f;
+    }
+    *scale = q7_block(x, reinterpret_cast<int *>(dst));
+}
+
+// Scratch::quantize's value matrices (Scratch::transpose, attention.rs:119-137) for every
+// (image, key head): row d of table t holds value[k][d] over the keys k, zeros to the padded
+// width; rows past head_dim to the quad are cleared. One thread per (table, block, row), rows
+// fastest so neighbouring threads read neighbouring channels.
+__global__ void value_table_kernel(const float *__restrict__ value, size_t stride, size_t offset, int kv_heads,
+                                   int keys, int hd, int rows4, int blocks, int8_t *__restrict__ codes,
+                                   float *__restrict__ scales, size_t tables)
+{
+    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= tables * rows4 * blocks) return;
+    const int row = int(id % rows4), b = int(id / rows4 % blocks);
+    const size_t t = id / (size_t(blocks) * rows4);
+    const size_t tb = (t * (rows4 / 4) + row / 4) * blocks + b;
+    int8_t *dst = codes + tb * 128 + (row % 4) * 32;
+    float *scale = scales + tb * 4 + row % 4;
+    if (row >= hd) {
+        clear_block(dst, scale);
+        return;
+    }
+    const size_t image = t / kv_heads, kh = t % kv_heads;
+    const float *src = value + image * size_t(keys) * stride + offset + kh * size_t(hd) + row;
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const int k = 32 * b + i;
+        x[i] = k < keys ? src[size_t(k) * stride] : 0.0f;
+    }
+    *scale = q7_block(x, reinterpret_cast<int *>(dst));
+}
+
+// The queries of every (image, head), quantized as the product quantizes its rows (quantize_rows,
+// matmul.rs:233-257, for a Q7b32 matrix: zero point 64) over the padded width pd, zeros past
+// head_dim: levels [u][r][pd], scales and corrections [u][r][pd / 32]. Eight lanes per group of 32.
+__global__ __launch_bounds__(256) void query_levels_kernel(const float *__restrict__ query, size_t stride,
+                                                           size_t offset, int heads, int queries, int hd, int pd,
+                                                           size_t slots, int8_t *__restrict__ levels,
+                                                           float *__restrict__ lscales, int32_t *__restrict__ lcorr)
+{
+    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int per_row = pd / 4;
+    const bool active = id < slots;
+    const int s4 = int(id % per_row);
+    const size_t rr = id / per_row;  // u · queries + r
+    const size_t u = rr / queries, r = rr % queries;
+    v4f v{0.0f, 0.0f, 0.0f, 0.0f};
+    if (active && 4 * s4 < hd) {
+        const size_t image = u / heads, h = u % heads;
+        const float *src = query + (image * size_t(queries) + r) * stride + offset + h * size_t(hd) + 4 * s4;
+        v = v4f{src[0], src[1], src[2], src[3]};
+    }
+    Group8 gr[1];
+    quantize_groups<1>(&v, gr);
+    if (active) store_group8(gr[0], 64, s4 / 8, levels + rr * pd, lscales + rr * (pd / 32), lcorr + rr * (pd / 32));
 }
 
 // One workgroup of four waves per query row: the row's scores (product · scale below keys4,
 // zeros to pk) staged in LDS, their maximum over the first `keys`, the exponentials there (all
-// 256 threads), and their sum in the scalar backend's order (scalar.rs:117-126, ops.rs:170-175):
-// lane o < 8 of the first wave sums offset o over the whole runs of eight in order, lane 0 adds
-// the rest in order, then the eight offset sums in order.
+// 256 threads), then two things at once: the first wave sums the exponentials in the scalar
+// backend's order (scalar.rs:117-126, ops.rs:170-175: lane o < 8 sums offset o over the whole
+// runs of eight in order, lane 0 adds the rest in order, then the eight offset sums in order),
+// and the other three quantize the row for the product with the values.
 template <bool FAST>
 __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restrict__ prod, int keys4, float scale,
-                                                           int keys, int pk, float *__restrict__ scores,
+                                                           int keys, int pk, int8_t *__restrict__ levels,
+                                                           float *__restrict__ level_scales, int32_t *__restrict__ level_corr,
                                                            float *__restrict__ sums)
 {
-    extern __shared__ float row[];  // [pk], then the four waves' maxima
+    extern __shared__ __align__(16) float row[];  // [pk], then the four waves' maxima
     float *wmax = row + pk;
+    v4f *row4 = reinterpret_cast<v4f *>(row);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t r = blockIdx.x;
+    const int n4 = pk / 4, k4 = keys4 / 4;
+    const v4f *src = reinterpret_cast<const v4f *>(prod + r * keys4);
     float m = -INFINITY;
-    for (int i = tid; i < pk; i += 256) {
-        const float v = i < keys4 ? prod[r * keys4 + i] * scale : 0.0f;
-        row[i] = v;
-        if (i < keys) m = fmaxf(m, v);
+    for (int s0 = 0; s0 < n4; s0 += 1024) {
+        v4f v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int slot = s0 + 256 * u + tid;
+            v[u] = slot < k4 ? src[slot] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int slot = s0 + 256 * u + tid;
+            if (slot < n4) {
+                const v4f x{v[u].x * scale, v[u].y * scale, v[u].z * scale, v[u].w * scale};
+                row4[slot] = x;
+                const int i = 4 * slot;
+                if (i < keys) m = fmaxf(m, x.x);
+                if (i + 1 < keys) m = fmaxf(m, x.y);
+                if (i + 2 < keys) m = fmaxf(m, x.z);
+                if (i + 3 < keys) m = fmaxf(m, x.w);
+            }
+        }
     }
     for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
     if (lane == 0) wmax[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    for (int i = tid; i < keys; i += 256) row[i] = FAST ? ref_exp_fast(row[i] - m) : ref_exp(row[i] - m);
+    for (int slot = tid; 4 * slot < keys; slot += 256) {
+        v4f x = row4[slot];
+        const int i = 4 * slot;
+        x.x = FAST ? ref_exp_fast(x.x - m) : ref_exp(x.x - m);
+        if (i + 1 < keys) x.y = FAST ? ref_exp_fast(x.y - m) : ref_exp(x.y - m);
+        if (i + 2 < keys) x.z = FAST ? ref_exp_fast(x.z - m) : ref_exp(x.z - m);
+        if (i + 3 < keys) x.w = FAST ? ref_exp_fast(x.w - m) : ref_exp(x.w - m);
+        row4[slot] = x;
+    }
     __syncthreads();
     if (wave == 0) {
         const int whole = keys / 8 * 8;
@@ -149,18 +283,30 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
             if (lane == 0) total = total + po;
         }
         if (lane == 0) sums[r] = total;
+        return;
     }
-    for (int i = tid; i < pk; i += 256) scores[r * pk + i] = row[i];
+    // The row, as the product with the values takes it: quantize_rows over its whole padded width
+    // for a Q7b32 matrix (zero point 64), eight lanes per group of 32, by the three other waves
+    // (slot ≡ thread mod 8, so each group of eight slots is eight aligned lanes of one wave).
+    for (int s0 = 0; s0 < n4; s0 += 192) {
+        const int slot = s0 + tid - 64;
+        const v4f v[1] = {slot < n4 ? row4[slot] : v4f{0.0f, 0.0f, 0.0f, 0.0f}};
+        Group8 gr[1];
+        quantize_groups<1>(v, gr);
+        if (slot < n4) store_group8(gr[0], 64, slot / 8, levels + r * pk, level_scales + r * (pk / 32), level_corr + r * (pk / 32));
+    }
 }
 
-// out[(first + r) · stride + d] = prod[r][d] / sums[r]
-__global__ void divide_kernel(const float *__restrict__ prod, const float *__restrict__ sums, int queries, int hd,
-                              float *__restrict__ out, size_t stride, size_t base)
+// out[(image · queries + r) · stride + h · hd + d] = pv[u][r][d] / sums[u][r] for every (image,
+// head) u = image · heads + h.
+__global__ void divide_kernel(const float *__restrict__ pv, const float *__restrict__ sums, int heads, int queries,
+                              int hd, size_t n, float *__restrict__ out, size_t stride)
 {
     const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= size_t(queries) * hd) return;
-    const int r = int(i / hd), d = int(i % hd);
-    out[base + size_t(r) * stride + d] = prod[i] / sums[r];
+    if (i >= n) return;
+    const size_t ur = i / hd, u = ur / queries, r = ur % queries, image = u / heads, h = u % heads;
+    const int d = int(i % hd);
+    out[(image * queries + r) * stride + h * hd + d] = pv[i] / sums[ur];
 }
 
 unsigned blocks_for(size_t n) { return unsigned((n + kThreads - 1) / kThreads); }
@@ -168,91 +314,165 @@ unsigned blocks_for(size_t n) { return unsigned((n + kThreads - 1) / kThreads); 
 // A query row per workgroup; a row of 16384 keys takes 64 KiB and 16 bytes of LDS, past the
 // default limit, which is then raised for the kernel on the current device.
 template <bool FAST>
-int launch_exponentials(const float *prod, int keys4, float scale, int keys, int pk, float *scores, float *sums,
-                        unsigned queries, hipStream_t st)
+int launch_exponentials(const float *prod, int keys4, float scale, int keys, int pk, int8_t *levels, float *level_scales,
+                        int32_t *level_corr, float *sums, unsigned queries, hipStream_t st)
 {
     const size_t smem = size_t(pk) * 4 + 16;
     if (smem > 64 * 1024)
         FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(exponentials_kernel<FAST>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    exponentials_kernel<FAST><<<queries, 256, smem, st>>>(prod, keys4, scale, keys, pk, scores, sums);
+    exponentials_kernel<FAST><<<queries, 256, smem, st>>>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums);
     FG_HIP(hipGetLastError());
     return FG_OK;
 }
 
-struct Scratch {
-    float *mean = nullptr, *krows = nullptr, *vrows = nullptr, *qrows = nullptr, *prod = nullptr, *scores = nullptr,
-          *sums = nullptr;
-    fg_table *keys = nullptr, *values = nullptr;
+// A run-time Q7b32 matrix (QuantizedMatrix) over caller-provided device storage: `rows` rows of
+// `cols` values, codes and scales in the device layout.
+fg_table runtime_matrix(int8_t *codes, float *scales, size_t rows, size_t cols)
+{
+    fg_table t{};
+    t.dtype = FG_Q7B32;
+    t.rows = rows;
+    t.cols = cols;
+    t.quads = (rows + 3) / 4;
+    t.blocks = t.groups = cols / 32;
+    t.code_bytes = t.quads * t.blocks * 128;
+    t.codes = codes;
+    t.scales = scales;
+    t.capacity = rows;
+    t.max_cols = cols;
+    return t;
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// The call's sizes.
+struct Shape {
+    size_t hd, keys, queries, pd, pk, keys4, kpad, kquads, vquads, ktables, qtables;
+    explicit Shape(const fg_attention *c)
+        : hd(c->head_dim), keys(c->keys), queries(c->queries), pd(pad32(hd)), pk(pad32(keys)), keys4((keys + 3) / 4 * 4),
+          kpad(keys4), kquads((keys + 3) / 4), vquads((hd + 3) / 4), ktables(c->images * c->kv_heads),
+          qtables(c->images * c->heads)
+    {
+    }
 };
 
-int run(const fg_attention *c, float *out, hipStream_t st, Scratch &w)
+// The call's scratch, carved from one allocation of the product's stream-ordered workspace pool:
+// no allocation reaches the driver and nothing waits for the stream. The key and value matrices
+// of every (image, key head) and the quantized queries of every (image, head) are built up front;
+// the scores, their levels and the products' outputs are per head.
+struct Scratch {
+    enum { KEYT, MEAN, KCODES, KSCALES, VCODES, VSCALES, QLEVELS, QSCALES, QCORR, PROD, ELEVELS, ESCALES, ECORR, SUMS, PV, N };
+    size_t size[N];
+    void *part[N];
+    explicit Scratch(const Shape &s)
+    {
+        size[KEYT] = s.ktables * s.hd * s.kpad * 4;
+        size[MEAN] = s.ktables * s.hd * 4;
+        size[KCODES] = s.ktables * s.kquads * (s.pd / 32) * 128;
+        size[KSCALES] = s.ktables * s.kquads * (s.pd / 32) * 16;
+        size[VCODES] = s.ktables * s.vquads * (s.pk / 32) * 128;
+        size[VSCALES] = s.ktables * s.vquads * (s.pk / 32) * 16;
+        size[QLEVELS] = s.qtables * s.queries * s.pd;
+        size[QSCALES] = size[QCORR] = s.qtables * s.queries * (s.pd / 32) * 4;
+        size[PROD] = s.queries * s.keys4 * 4;
+        size[ELEVELS] = s.queries * s.pk;
+        size[ESCALES] = size[ECORR] = s.queries * (s.pk / 32) * 4;
+        size[SUMS] = s.qtables * s.queries * 4;
+        size[PV] = s.qtables * s.queries * s.hd * 4;
+    }
+    size_t total() const
+    {
+        size_t n = 0;
+        for (size_t b : size) n += align256(b);
+        return n;
+    }
+    void carve(void *ws)
+    {
+        char *at = static_cast<char *>(ws);
+        for (int i = 0; i < N; i++) {
+            part[i] = at;
+            at += align256(size[i]);
+        }
+    }
+    template <class T> T *at(int i) const { return static_cast<T *>(part[i]); }
+};
+
+int run(const fg_attention *c, float *out, hipStream_t st, const Shape &s, const Scratch &w)
 {
-    const int hd = int(c->head_dim), keys = int(c->keys), queries = int(c->queries);
-    const int pd = int(pad32(c->head_dim)), pk = int(pad32(c->keys)), keys4 = (keys + 3) / 4 * 4;
+    const int hd = int(s.hd), keys = int(s.keys), queries = int(s.queries), pd = int(s.pd), pk = int(s.pk);
+    const int keys4 = int(s.keys4), kpad = int(s.kpad);
     const size_t group = c->heads / c->kv_heads, stride = c->heads * c->head_dim;
     const float scale = 1.0f / sqrtf(float(hd));
-    const size_t bytes[] = {c->images * c->kv_heads * size_t(hd) * 4, size_t(keys) * pd * 4,
-                            size_t(hd) * pk * 4, size_t(queries) * pd * 4,
-                            size_t(queries) * size_t(keys4 > hd ? keys4 : hd) * 4,
-                            size_t(queries) * pk * 4, size_t(queries) * 4};
-    float **ptrs[] = {&w.mean, &w.krows, &w.vrows, &w.qrows, &w.prod, &w.scores, &w.sums};
-    for (int i = 0; i < 7; i++) FG_HIP(hipMallocAsync(reinterpret_cast<void **>(ptrs[i]), bytes[i], st));
-    int rc;
-    if ((rc = fg_qmatrix_create(size_t(keys), size_t(pd), &w.keys)) || (rc = fg_qmatrix_create(size_t(hd), size_t(pk), &w.values)))
-        return rc;
-    key_mean_kernel<<<blocks_for(c->images * c->kv_heads * size_t(hd)), kThreads, 0, st>>>(
-        c->key, c->key_stride, c->key_offset, int(c->images), int(c->kv_heads), keys, hd, w.mean);
+    // Scratch::quantize (attention.rs:100-137) for every (image, key head): the keys' mean over
+    // the keys in order, the keys less their mean and the values transposed as Q7b32 matrices
+    const dim3 tiles(unsigned((keys + 63) / 64), unsigned((hd + 63) / 64), unsigned(s.ktables));
+    key_transpose_kernel<<<tiles, 256, 0, st>>>(c->key, c->key_stride, c->key_offset, int(c->kv_heads), keys, hd, kpad,
+                                                w.at<float>(Scratch::KEYT));
+    key_mean_kernel<<<unsigned(s.ktables * s.hd), 64, size_t((kpad + 4095) / 4096 * 4096) * 4, st>>>(
+        w.at<float>(Scratch::KEYT), keys, kpad, w.at<float>(Scratch::MEAN));
+    const size_t kthreads = s.ktables * s.kquads * 4 * (s.pd / 32), vthreads = s.ktables * s.vquads * 4 * (s.pk / 32);
+    key_table_kernel<<<blocks_for(kthreads), kThreads, 0, st>>>(
+        c->key, c->key_stride, c->key_offset, int(c->kv_heads), keys, hd, int(s.kquads * 4), pd / 32,
+        w.at<float>(Scratch::MEAN), w.at<int8_t>(Scratch::KCODES), w.at<float>(Scratch::KSCALES), s.ktables);
+    value_table_kernel<<<blocks_for(vthreads), kThreads, 0, st>>>(
+        c->value, c->value_stride, c->value_offset, int(c->kv_heads), keys, hd, int(s.vquads * 4), pk / 32,
+        w.at<int8_t>(Scratch::VCODES), w.at<float>(Scratch::VSCALES), s.ktables);
+    const size_t slots = s.qtables * s.queries * (s.pd / 4);
+    query_levels_kernel<<<blocks_for(slots), kThreads, 0, st>>>(
+        c->query, c->query_stride, c->query_offset, int(c->heads), queries, hd, pd, slots,
+        w.at<int8_t>(Scratch::QLEVELS), w.at<float>(Scratch::QSCALES), w.at<int32_t>(Scratch::QCORR));
     FG_HIP(hipGetLastError());
+    int rc;
     for (size_t image = 0; image < c->images; image++) {
         for (size_t kh = 0; kh < c->kv_heads; kh++) {
-            // Scratch::quantize (attention.rs:100-137)
-            const size_t kbase = image * c->keys * c->key_stride + c->key_offset + kh * c->head_dim;
-            const size_t vbase = image * c->keys * c->value_stride + c->value_offset + kh * c->head_dim;
-            key_rows_kernel<<<blocks_for(size_t(keys) * pd), kThreads, 0, st>>>(
-                c->key, c->key_stride, kbase, keys, hd, pd, w.mean + (image * c->kv_heads + kh) * size_t(hd), w.krows);
-            value_rows_kernel<<<blocks_for(size_t(hd) * pk), kThreads, 0, st>>>(c->value, c->value_stride, vbase, keys, hd,
-                                                                                pk, w.vrows);
-            FG_HIP(hipGetLastError());
-            if ((rc = fg_qmatrix_reset(w.keys, size_t(pd))) || (rc = fg_qmatrix_extend(w.keys, size_t(keys), st)) ||
-                (rc = fg_qmatrix_set_rows(w.keys, 0, size_t(keys), w.krows, st)) ||
-                (rc = fg_qmatrix_reset(w.values, size_t(pk))) || (rc = fg_qmatrix_extend(w.values, size_t(hd), st)) ||
-                (rc = fg_qmatrix_set_rows(w.values, 0, size_t(hd), w.vrows, st)))
-                return rc;
+            const size_t t = image * c->kv_heads + kh;
+            fg_table ktab = runtime_matrix(w.at<int8_t>(Scratch::KCODES) + t * s.kquads * (s.pd / 32) * 128,
+                                           w.at<float>(Scratch::KSCALES) + t * s.kquads * (s.pd / 32) * 4, s.keys, s.pd);
+            fg_table vtab = runtime_matrix(w.at<int8_t>(Scratch::VCODES) + t * s.vquads * (s.pk / 32) * 128,
+                                           w.at<float>(Scratch::VSCALES) + t * s.vquads * (s.pk / 32) * 4, s.hd, s.pk);
             for (size_t h = kh * group; h < (kh + 1) * group; h++) {
                 // Scratch::unit (attention.rs:157-214) for every query of the image at once
-                const size_t qbase = image * c->queries * c->query_stride + c->query_offset + h * c->head_dim;
-                query_rows_kernel<<<blocks_for(size_t(queries) * pd), kThreads, 0, st>>>(c->query, c->query_stride, qbase,
-                                                                                         queries, hd, pd, w.qrows);
-                FG_HIP(hipGetLastError());
+                const size_t u = image * c->heads + h;
                 ProductArgs a{};
-                a.t = w.keys;
-                a.x = w.qrows;
-                a.rows = size_t(queries);
+                a.t = &ktab;
+                a.q = w.at<int8_t>(Scratch::QLEVELS) + u * s.queries * s.pd;
+                a.as = w.at<float>(Scratch::QSCALES) + u * s.queries * (s.pd / 32);
+                a.corr = w.at<int32_t>(Scratch::QCORR) + u * s.queries * (s.pd / 32);
+                a.rows = s.queries;
                 a.quad_begin = 0;
                 a.quad_end = size_t(keys4 / 4);
-                a.out = w.prod;
+                a.out = w.at<float>(Scratch::PROD);
                 a.ld_out = size_t(keys4);
                 if ((rc = launch_product(a, st))) return rc;
+                float *sums = w.at<float>(Scratch::SUMS) + u * s.queries;
                 rc = c->exponentials == FG_EXP_FAST
-                         ? launch_exponentials<true>(w.prod, keys4, scale, keys, pk, w.scores, w.sums, unsigned(queries), st)
-                         : launch_exponentials<false>(w.prod, keys4, scale, keys, pk, w.scores, w.sums, unsigned(queries), st);
+                         ? launch_exponentials<true>(w.at<float>(Scratch::PROD), keys4, scale, keys, pk,
+                                                     w.at<int8_t>(Scratch::ELEVELS), w.at<float>(Scratch::ESCALES),
+                                                     w.at<int32_t>(Scratch::ECORR), sums, unsigned(queries), st)
+                         : launch_exponentials<false>(w.at<float>(Scratch::PROD), keys4, scale, keys, pk,
+                                                      w.at<int8_t>(Scratch::ELEVELS), w.at<float>(Scratch::ESCALES),
+                                                      w.at<int32_t>(Scratch::ECORR), sums, unsigned(queries), st);
                 if (rc) return rc;
                 ProductArgs b{};
-                b.t = w.values;
-                b.x = w.scores;
-                b.rows = size_t(queries);
+                b.t = &vtab;
+                b.q = w.at<int8_t>(Scratch::ELEVELS);
+                b.as = w.at<float>(Scratch::ESCALES);
+                b.corr = w.at<int32_t>(Scratch::ECORR);
+                b.rows = s.queries;
                 b.quad_begin = 0;
                 b.quad_end = size_t(hd / 4);
-                b.out = w.prod;
-                b.ld_out = size_t(hd);
+                b.out = w.at<float>(Scratch::PV) + u * s.queries * s.hd;
+                b.ld_out = s.hd;
                 if ((rc = launch_product(b, st))) return rc;
-                divide_kernel<<<blocks_for(size_t(queries) * hd), kThreads, 0, st>>>(
-                    w.prod, w.sums, queries, hd, out, stride, image * c->queries * stride + h * c->head_dim);
-                FG_HIP(hipGetLastError());
             }
         }
     }
+    // each output divided by its row's sum, every head at once
+    const size_t n = s.qtables * s.queries * s.hd;
+    divide_kernel<<<blocks_for(n), kThreads, 0, st>>>(w.at<float>(Scratch::PV), w.at<float>(Scratch::SUMS), int(c->heads),
+                                                      queries, hd, n, out, stride);
+    FG_HIP(hipGetLastError());
     return FG_OK;
 }
 
@@ -267,7 +487,8 @@ extern "C" int fg_attend(const fg_attention *c, float *out, void *stream)
     if (!c->heads || !c->kv_heads || !c->head_dim || !c->images || !c->queries || !c->keys || c->heads % c->kv_heads)
         return set_error(FG_ERR_SHAPE, "fg_attend: heads, key heads, head_dim, images, queries and keys must be positive, "
                                        "the heads a multiple of the key heads");
-    if (c->head_dim % 4) return set_error(FG_ERR_SHAPE, "fg_attend: head_dim must be whole quads");
+    if (c->head_dim % 4 || c->head_dim > size_t(kMaxHeadDim))
+        return set_error(FG_ERR_SHAPE, "fg_attend: head_dim must be whole quads, at most 1024");
     if (c->exponentials != FG_EXP_EXACT && c->exponentials != FG_EXP_FAST)
         return set_error(FG_ERR_ARG, "fg_attend: exponentials must be FG_EXP_EXACT or FG_EXP_FAST");
     if (pad32(c->keys) * 4 > size_t(kMaxRowBytes)) return set_error(FG_ERR_SHAPE, "fg_attend: at most 16384 keys");
@@ -277,15 +498,14 @@ extern "C" int fg_attend(const fg_attention *c, float *out, void *stream)
         c->value_offset + c->kv_heads * c->head_dim > c->value_stride)
         return set_error(FG_ERR_SHAPE, "fg_attend: an operand's heads run past its row stride");
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    Scratch w;
-    int rc = run(c, out, st, w);
-    // the scratch is ordered on the stream; the run-time matrices are freed once it has finished
-    float *ptrs[] = {w.mean, w.krows, w.vrows, w.qrows, w.prod, w.scores, w.sums};
-    for (float *p : ptrs)
-        if (p) (void)hipFreeAsync(p, st);
-    const hipError_t e = hipStreamSynchronize(st);
-    if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipStreamSynchronize");
-    if (w.keys) (void)fg_table_free(w.keys);
-    if (w.values) (void)fg_table_free(w.values);
+    const Shape s(c);
+    Scratch w(s);
+    void *ws = nullptr;
+    FG_HIP(workspace_alloc(&ws, w.total(), st));
+    w.carve(ws);
+    int rc = run(c, out, st, s, w);
+    // the scratch goes back to the pool in stream order, after the call's last kernel
+    const hipError_t e = hipFreeAsync(ws, st);
+    if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
     return rc;
 }

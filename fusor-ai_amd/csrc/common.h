@@ -281,6 +281,29 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d)
     return (a & 0xff) | ((b & 0xff) << 8) | ((c & 0xff) << 16) | ((d & 0xff) << 24);
 }
 
+// One block of 32 values of a run-time Q7b32 matrix (QuantizedMatrix::set_block, matmul.rs:77-90):
+// the scale absmax / 63 (1 for a zero block), the levels rint(x / scale) saturated to i8 and
+// clamped to ±63, stored signed four to a dword (the device form u − 64 of the codes u).
+__device__ __forceinline__ float q7_block(const float *x, int *dst)
+{
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
+    const float scale = group_scale(amax, 63.0f);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int l[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float v = __builtin_rintf(x[4 * i + j] / scale);
+            const int level = v != v ? 0 : v >= 127.0f ? 127 : v <= -128.0f ? -128 : int(v);
+            l[j] = level < -63 ? -63 : (level > 63 ? 63 : level);
+        }
+        dst[i] = pack4(l[0], l[1], l[2], l[3]);
+    }
+    return scale;
+}
+
 // Offset-binary nibbles (u in [0,15]) of a dword to signed levels u - 8, byte-wise without
 // borrows: (u + 0x78) ^ 0x80 == u - 8 as an int8.
 __device__ __forceinline__ int nibbles_signed(int packed_nibbles)
@@ -330,6 +353,8 @@ struct ProductArgs {
 };
 // Scratch bytes a product needs beyond its inputs and outputs (0 for the matrix-vector rows).
 size_t product_scratch_bytes(const ProductArgs &a);
+// A stream-ordered allocation from this device's workspace pool (kept across calls).
+hipError_t workspace_alloc(void **ptr, size_t bytes, hipStream_t s);
 int launch_matvec(const ProductArgs &a, hipStream_t s);
 int launch_gemm(const ProductArgs &a, hipStream_t s);
 int launch_t2(const ProductArgs &a, hipStream_t s);

@@ -219,12 +219,7 @@ __global__ void qmatrix_set_kernel(int8_t *__restrict__ codes, float *__restrict
         x[4 * i + 2] = f.z;
         x[4 * i + 3] = f.w;
     }
-    uint8_t u[128];
-    const float scale = quantize_group(FG_Q7B32, x, 32, u);
-    int *dst = reinterpret_cast<int *>(codes + (quad * blocks + b) * 128 + lane * 32);
-    for (int i = 0; i < 8; i++)
-        dst[i] = pack4(int(u[4 * i]) - 64, int(u[4 * i + 1]) - 64, int(u[4 * i + 2]) - 64, int(u[4 * i + 3]) - 64);
-    scales[(quad * blocks + b) * 4 + lane] = scale;
+    scales[(quad * blocks + b) * 4 + lane] = q7_block(x, reinterpret_cast<int *>(codes + (quad * blocks + b) * 128 + lane * 32));
 }
 
 }  // namespace

@@ -159,7 +159,8 @@ typedef struct fg_attention {
 /* attention::attend (blocks/src/attention.rs:81-214) for the whole call, into device `out`
  * [images * queries][heads * head_dim]: keys and values quantized at run time (Q7b32 rows),
  * both products on the quantized kernels, the reference's f32 order around them. head_dim whole
- * quads, at most 16384 keys. Returns once the work on `stream` has finished. */
+ * quads, at most 1024; at most 16384 keys. The work is ordered on `stream` (its scratch comes
+ * from and returns to a stream-ordered pool): `out` is ready once the stream's work is. */
 int fg_attend(const fg_attention *call, float *out, void *stream);
 
 /* ------------------------------------------------------------------------ activations */

@@ -26,6 +26,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
 struct GemmParams {
@@ -460,100 +461,177 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     }
 }
 
-// At most 16 rows over many columns (the int4 14336 x 4096 case): four waves per workgroup,
-// each a 16 x 16 tile of four adjacent column tiles, share the 16 activation rows, staged in LDS
-// one slab of kSlabBlocks blocks at a time with coalesced 16-byte loads (rows padded by 32 bytes
-// so the waves' reads spread over the banks), with the slab's activation scales. Each wave's
-// requests per block are then its weights and their scales only; the groups run in order and
-// the arithmetic is gemm16_kernel's. No scheduling barrier between blocks: the compiler overlaps
-// one block's LDS reads and product with the previous block's rescale (16 x 4096 -> 14336 Q4:
-// 27.5 us with one wave per tile, 22.0 with the slab and a barrier per block, 19.4 without).
-constexpr int kSlabBlocks = 64;
-constexpr int kSlabRow = kSlabBlocks * 32 + 32;  // bytes per staged row
-constexpr int kSlabDepth = 8;  // blocks of weights in flight per wave (16 measured no faster)
+// At most 16 rows over many columns, streamed: a workgroup of four waves owns 64 columns (16
+// quads), wave w the 16 x 16 tile of quads 4w .. 4w + 3. The operands of kStreamBlocks blocks (a
+// stage) arrive by direct global-to-LDS loads (lane l of a load writes 16 bytes, or 4, at its base
+// + 16·l, or 4·l), DEPTH - 1 stages ahead of the stage being multiplied, so tens of kilobytes per
+// workgroup are in flight with no register held for them. In every load four neighbouring lanes
+// read one run of bytes (lanes that each touch another line cost the address unit a cycle apiece),
+// and every layout spreads a wave's reads of a block over the banks:
+//   W  [16 quads][kStreamBlocks][QB]  the quads' weight bytes, a quad's run of blocks being one run
+//                                     of bytes in the table; a quad every WQ bytes;
+//   WS [4 waves][4 quads][16 slots][4] the weight scales of a quad's blocks, slot k holding block
+//                                     k + 2·quad (mod 16): the four quads' reads of one block fall
+//                                     on different banks;
+//   A  [8 groups][16 rows][4][16 B]   the activation levels, group g holding bytes 64g .. 64g + 63
+//                                     of each row's stage, row r's piece p at position p ^ (r/2 % 4):
+//                                     the 16 rows' pieces of a block fall on eight bank offsets;
+//   AS [4 groups][16 rows][4]         the activation scales, group j holding blocks 4j .. 4j + 3.
+// Each wave waits for its own loads of a stage, then one barrier publishes the stage and frees the
+// buffer the next issue refills. Rows and columns past the edges re-read the last valid one;
+// blocks past the last are loaded clamped (in bounds) and skipped. The arithmetic is
+// gemm16_kernel's.
+constexpr int kStreamBlocks = 16;
 
 template <int FMT>
-__global__ __launch_bounds__(256) void gemm16_slab_kernel(GemmParams p)
+struct StreamTile {
+    static constexpr int QB = FMT == 8 ? 128 : 64;             // device bytes per quad block
+    static constexpr int WQ = kStreamBlocks * QB + 64;         // a quad's stage bytes, padded
+    static constexpr int W_BYTES = 16 * WQ;
+    static constexpr int WS_BYTES = 4 * kStreamBlocks * 4 * 16;
+    static constexpr int A_BYTES = kStreamBlocks * 32 * 16;
+    static constexpr int AS_BYTES = kStreamBlocks * 16 * 4;
+    static constexpr int STAGE = W_BYTES + WS_BYTES + A_BYTES + AS_BYTES;
+    static constexpr int DEPTH = FMT == 8 ? 3 : 4;             // stages in LDS
+    static constexpr int W_LOADS = kStreamBlocks * QB / 1024;  // per quad
+    static constexpr int LOADS = 4 * W_LOADS + 1 + 2 + 1;      // per wave and stage
+    static constexpr int LDS = DEPTH * STAGE;
+    static_assert(LDS <= 160 * 1024 && (DEPTH - 2) * LOADS < 64, "stream tile");
+};
+
+template <int FMT>
+__global__ __launch_bounds__(256) void gemm16_stream_kernel(GemmParams p)
 {
-    extern __shared__ __align__(16) unsigned char slab_lds[];
-    int8_t *slab = reinterpret_cast<int8_t *>(slab_lds);                       // [16][kSlabRow]
-    float *sscales = reinterpret_cast<float *>(slab_lds + 16 * kSlabRow);     // [kSlabBlocks][16]
-    constexpr int QB = FMT == 8 ? 128 : 64;
-    const int tid = threadIdx.x, lane = tid & 63, i = lane & 15, s = lane >> 4;
+    using T = StreamTile<FMT>;
+    constexpr int QB = T::QB, WQ = T::WQ, DEPTH = T::DEPTH, KS = kStreamBlocks, kWLoads = T::W_LOADS;
+    constexpr int kStage = T::STAGE, kW = T::W_BYTES, kWS = T::WS_BYTES, kA = T::A_BYTES;
+    extern __shared__ __align__(16) unsigned char stream_lds[];  // [DEPTH][STAGE]
+    const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, s = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int tx, ty;
     tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 63) / 64, (p.M + 15) / 16, tx, ty);
-    const int m0 = ty * 16, n = p.col_begin + tx * 64 + wave * 16 + i, nc = min(n, p.col_end - 1);
-    const int B = p.B;
-    const int8_t *wrow = p.codes + size_t(nc >> 2) * B * QB + (nc & 3) * (QB / 4) + (FMT == 8 ? 8 * s : 8 * (s & 1));
-    const int shift = FMT == 8 ? 0 : 4 * (s >> 1);
-    const float *wsrow = p.wscales + size_t(nc >> 2) * p.G * 4 + (nc & 3);
-    long rw[kSlabDepth];
-    float rs[kSlabDepth];
+    const int m0 = ty * 16, q0 = (p.col_begin >> 2) + tx * 16, last_quad = (p.col_end - 1) >> 2;
+    const int B = p.B, G = p.G, K = p.K;
+    const int stages = (B + KS - 1) / KS;
+
+    auto issue = [&](int st, int buf) {
+        unsigned char *base = stream_lds + buf * kStage;
+        const int b0 = st * KS;
+        // this wave's four quads' weight bytes (clamped to the quad's last 16 bytes)
 #pragma unroll
-    for (int k = 0; k < kSlabDepth; k++) {
-        const int bb = min(k, B - 1);
-        rw[k] = *reinterpret_cast<const long *>(wrow + size_t(bb) * QB);
-        rs[k] = wsrow[size_t(bb) * 4];
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = 0; s0 < B; s0 += kSlabBlocks) {
-        const int nb = min(kSlabBlocks, B - s0);
-        __syncthreads();  // every wave is done with the previous slab
+        for (int qq = 0; qq < 4; qq++) {
+            const int8_t *qbase = p.codes + size_t(min(q0 + 4 * wave + qq, last_quad)) * B * QB;
+#pragma unroll
+            for (int j = 0; j < kWLoads; j++) {
+                const int at = min(b0 * QB + (j * 64 + lane) * 16, B * QB - 16);
+                __builtin_amdgcn_global_load_lds(qbase + at, base + (4 * wave + qq) * WQ + j * 1024, 16, 0, 0);
+            }
+        }
         {
-            // 16 rows x kSlabBlocks·32 bytes in 16-byte pieces (past the row's end: its last
-            // piece again, unused), then the slab's scales, 4 blocks of one row per thread
-            v4i piece[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int q = tid + 256 * j, r = q >> 7, c = q & 127;
-                const int at = min(s0 * 32 + c * 16, p.K - 16);
-                piece[j] = *reinterpret_cast<const v4i *>(p.q + size_t(min(m0 + r, p.M - 1)) * p.K + at);
-            }
-            const int r = tid & 15, c4 = tid >> 4;
-            const v4f sv = *reinterpret_cast<const v4f *>(p.as + size_t(min(m0 + r, p.M - 1)) * p.G + min(s0 + 4 * c4, B - 4));
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int q = tid + 256 * j, rr = q >> 7, c = q & 127;
-                *reinterpret_cast<v4i *>(slab + rr * kSlabRow + c * 16) = piece[j];
-            }
-            sscales[(4 * c4) * 16 + r] = sv.x;
-            sscales[(4 * c4 + 1) * 16 + r] = sv.y;
-            sscales[(4 * c4 + 2) * 16 + r] = sv.z;
-            sscales[(4 * c4 + 3) * 16 + r] = sv.w;
+            // weight scales: lane l, quad 4·wave + l / 16, slot l % 16 (block slot + 2·quad mod 16)
+            const int qw = lane >> 4, slot = lane & 15;
+            const int q = min(q0 + 4 * wave + qw, last_quad), blk = min(b0 + ((slot + 2 * qw) & 15), B - 1);
+            __builtin_amdgcn_global_load_lds(p.wscales + (size_t(q) * G + blk) * 4, base + kW + wave * 1024, 16, 0, 0);
         }
-        __syncthreads();
-        for (int b = s0; b < s0 + nb; b += kSlabDepth) {
 #pragma unroll
-            for (int k = 0; k < kSlabDepth; k++) {
-                const int bb = b + k;
-                // past the last block: clamped operands and a +0 term, which leaves the sum
-                // (never -0) as it is
-                const bool live = bb < B;
-                long w = rw[k];
-                if (FMT == 4) {
-                    const int lo = nibbles_signed(int(w) >> shift), hi = nibbles_signed(int(w >> 32) >> shift);
-                    w = long(unsigned(lo)) | (long(hi) << 32);
-                }
-                const int sb = min(bb, B - 1) - s0;  // < kSlabBlocks
-                const long a = *reinterpret_cast<const long *>(slab + i * kSlabRow + sb * 32 + 8 * s);
-                const v4i zero = {0, 0, 0, 0};
-                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, w, zero, 0, 0, 0);
-                const float ws = rs[k];
-                const v4f sc = *reinterpret_cast<const v4f *>(sscales + sb * 16 + 4 * s);
-                const float d0 = live ? float(d[0]) : 0.0f, d1 = live ? float(d[1]) : 0.0f;
-                const float d2 = live ? float(d[2]) : 0.0f, d3 = live ? float(d[3]) : 0.0f;
-                acc[0] = acc[0] + d0 * (ws * sc.x);
-                acc[1] = acc[1] + d1 * (ws * sc.y);
-                acc[2] = acc[2] + d2 * (ws * sc.z);
-                acc[3] = acc[3] + d3 * (ws * sc.w);
-                const int nw = min(bb + kSlabDepth, B - 1);
-                rw[k] = *reinterpret_cast<const long *>(wrow + size_t(nw) * QB);
-                rs[k] = wsrow[size_t(nw) * 4];
+        for (int j = 0; j < 2; j++) {
+            // activation group g = 2·wave + j: lane l, row r = l / 4, position l % 4 holding piece
+            // (l % 4) ^ (r / 2 % 4)
+            const int g = 2 * wave + j, r = lane >> 2, piece = (lane & 3) ^ ((r >> 1) & 3);
+            const int row = min(m0 + r, p.M - 1), at = min(b0 * 32 + (4 * g + piece) * 16, K - 16);
+            __builtin_amdgcn_global_load_lds(p.q + size_t(row) * K + at, base + kW + kWS + g * 1024, 16, 0, 0);
+        }
+        {
+            // activation scales of group `wave`: lane l, row l / 4, block 4·wave + l % 4
+            const int row = min(m0 + (lane >> 2), p.M - 1), blk = min(b0 + 4 * wave + (lane & 3), B - 1);
+            __builtin_amdgcn_global_load_lds(p.as + size_t(row) * G + blk, base + kW + kWS + kA + wave * 256, 4, 0, 0);
+        }
+    };
+
+    const int shift = FMT == 8 ? 0 : 4 * (s >> 1);
+    const int w_off = (4 * wave + (c >> 2)) * WQ + (c & 3) * (QB / 4) + (FMT == 8 ? 8 * s : 8 * (s & 1));
+    // block b of row c: group b / 2, piece 2·(b % 2) + s / 2 at position piece ^ (c / 2 % 4)
+    const int a_row = kW + kWS + c * 64 + 8 * (s & 1), sig = (c >> 1) & 3;
+    const int a_off0 = a_row + ((s >> 1) ^ sig) * 16, a_off1 = a_row + ((2 + (s >> 1)) ^ sig) * 16;
+    // the scale products' operands: lane l gives block 4j + l / 16's scale of row (or column)
+    // l % 16; the weight scale of column i, block k sits in quad i / 4's slot k - 2·(i / 4)
+    const int blk4 = lane >> 4, qi = c >> 2;
+    const int as_off = kW + kWS + kA + (c * 4 + blk4) * 4;
+    const int ws_row = kW + wave * 1024 + qi * 256 + (c & 3) * 4;
+
+    // One stage's operands in registers: with one wave per SIMD nothing hides a read's latency but
+    // the wave's own other work, so a stage's reads go out before the previous stage's rescale.
+    struct Ops {
+        long w[KS], a[KS];
+        float as[KS / 4], ws[KS / 4];
+    };
+    // The products of a stage: the int8 group sums, and the scale products fl(ws·as) of four
+    // blocks at a time from one f32 MFMA outer product (v_mfma_f32_16x16x1_4b: block k of the four
+    // in results 4k .. 4k + 3, the layout of the int8 sums; exactly the VALU's rounded products).
+    struct Prods {
+        v4i d[KS];
+        v16f p[KS / 4];
+    };
+    auto read = [&](const unsigned char *base, Ops &o) {
+#pragma unroll
+        for (int b = 0; b < KS; b++) {
+            o.w[b] = *reinterpret_cast<const long *>(base + w_off + b * QB);
+            o.a[b] = *reinterpret_cast<const long *>(base + (b & 1 ? a_off1 : a_off0) + (b >> 1) * 1024);
+        }
+#pragma unroll
+        for (int j = 0; j < KS / 4; j++) {
+            o.as[j] = *reinterpret_cast<const float *>(base + as_off + j * 256);
+            o.ws[j] = *reinterpret_cast<const float *>(base + ws_row + ((4 * j + blk4 - 2 * qi) & 15) * 16);
+        }
+    };
+    auto multiply = [&](const Ops &o, Prods &r) {
+#pragma unroll
+        for (int j = 0; j < KS / 4; j++) {
+            const v16f zero16 = {0};
+            r.p[j] = __builtin_amdgcn_mfma_f32_16x16x1f32(o.as[j], o.ws[j], zero16, 0, 0, 0);
+        }
+#pragma unroll
+        for (int b = 0; b < KS; b++) {
+            long x = o.w[b];
+            if (FMT == 4) {
+                const int lo = nibbles_signed(int(x) >> shift), hi = nibbles_signed(int(x >> 32) >> shift);
+                x = long(unsigned(lo)) | (long(hi) << 32);
+            }
+            const v4i zero = {0, 0, 0, 0};
+            r.d[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[b], x, zero, 0, 0, 0);
+        }
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // the terms in group order; blocks past the last skipped (a uniform branch, last stage only)
+    auto rescale = [&](const Prods &r, int live) {
+#pragma unroll
+        for (int b = 0; b < KS; b++) {
+            if (b < live) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] = acc[v] + float(r.d[b][v]) * r.p[b / 4][4 * (b % 4) + v];
             }
         }
+    };
+
+#pragma unroll
+    for (int k = 0; k < DEPTH - 1; k++)
+        if (k < stages) issue(k, k);
+    Prods prev;
+    int prev_live = 0;
+    for (int st = 0; st < stages; st++) {
+        // this wave's loads of stage st: the later stages issued so far may still be in flight
+        if (st + DEPTH - 2 < stages) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((DEPTH - 2) * T::LOADS) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // every wave's loads of stage st; every wave done reading stage st - 1
+        if (st + DEPTH - 1 < stages) issue(st + DEPTH - 1, (st + DEPTH - 1) % DEPTH);
+        Ops o;
+        read(stream_lds + (st % DEPTH) * kStage, o);
+        if (st > 0) rescale(prev, prev_live);  // while the reads are in flight
+        multiply(o, prev);
+        prev_live = min(KS, B - st * KS);
     }
+    rescale(prev, prev_live);
+    const int n = p.col_begin + tx * 64 + wave * 16 + c;
     if (n >= p.col_end) return;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
@@ -855,10 +933,13 @@ int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
             FG_HIP(hipGetLastError());
             return FG_OK;
         }
-        // more tiles: four adjacent column tiles per workgroup share the activation rows in LDS
-        if (!dots && !FUSED && p.B % 4 == 0 && p.K % 16 == 0 && p.B >= 4) {
+        // more tiles: four adjacent column tiles per workgroup, their operands streamed through LDS
+        if (!dots && !FUSED) {
             const dim3 sgrid(unsigned(((ncols + 63) / 64) * ((p.M + 15) / 16)));
-            gemm16_slab_kernel<FMT><<<sgrid, 256, size_t(16 * kSlabRow + kSlabBlocks * 16 * 4), s>>>(p);
+            constexpr int lds = StreamTile<FMT>::LDS;
+            FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm16_stream_kernel<FMT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+            gemm16_stream_kernel<FMT><<<sgrid, 256, size_t(lds), s>>>(p);
             FG_HIP(hipGetLastError());
             return FG_OK;
         }

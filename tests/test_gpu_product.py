@@ -388,17 +388,17 @@ def test_int4_shape_bit_exact(fk, rows):
     t = table(fk, O.Q4B32, n, k, data)
     x = activations(rows, k, seed=44)
     got = gpu_product(fk, t, x, rows)
-    sample = list(range(rows)) if rows <= 2 else [0, 5, 15]
-    want = oracle_product(O.Q4B32, n, k, data, x[sample], len(sample))
-    assert same_bits(got[sample], want), first_mismatch(got[sample], want)
+    q, s, c = O.quantize_rows(x.reshape(-1), O.Q4B32)
+    want = O.matmul_threaded(O.Q4B32, n, k, data, q, s, c, rows, threads=16)
+    assert same_bits(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
 @pytest.mark.parametrize("rows", [5, 16])
-def test_small_batch_with_staged_rows_over_many_columns(fk, dtype, rows):
+def test_small_batch_streamed_over_many_columns(fk, dtype, rows):
     """5-16 rows over 515 tiles of 16 columns (the last workgroup's columns partly past the
-    table): the activation rows staged in LDS in slabs of 64 blocks, a whole slab and a partial
-    one of 8."""
+    table): the operands streamed through LDS in stages of 16 blocks, four whole stages and a
+    partial one of 8; then a column range starting inside the table, with bias."""
     n, k = 8228, 32 * 72
     data = synthetic_table(dtype, n, k, seed=rows + 17)
     t = table(fk, dtype, n, k, data)
@@ -407,6 +407,23 @@ def test_small_batch_with_staged_rows_over_many_columns(fk, dtype, rows):
     got = gpu_product(fk, t, x, rows, bias=bias)
     want = oracle_product(dtype, n, k, data, x, rows, bias=bias)
     assert same_bits(got, want), first_mismatch(got, want)
+    got = gpu_product(fk, t, x, rows, cols=range(36, n), bias=bias)
+    assert same_bits(got, oracle_product(dtype, n, k, data, x, rows, 36, n, bias=bias))
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+def test_small_batch_streamed_scale_products_below_the_normal_range(fk, dtype):
+    """The streamed small-batch product forms fl(ws * as) with an f32 MFMA outer product: weight
+    scales near 1e-8 and activations near 1e-30 make every such product subnormal, while the
+    terms fl(D * p) are normal; the MFMA must round them as the VALU multiply does."""
+    n, k, rows = 8228, 32 * 40, 16
+    data = synthetic_table(dtype, n, k, seed=dtype + 40, scale_lo=1e-9, scale_hi=1e-8)
+    t = table(fk, dtype, n, k, data)
+    x = (activations(rows, k, seed=41) * np.float32(1e-30)).astype(np.float32)
+    got = gpu_product(fk, t, x, rows)
+    want = oracle_product(dtype, n, k, data, x, rows)
+    assert same_bits(got, want), first_mismatch(got, want)
+    assert np.all(np.isfinite(want)) and np.any(want != 0)
 
 
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])

@@ -48,36 +48,44 @@ constexpr int kThreads = 256;
 __device__ __forceinline__ int dot16(int4 w, int4 a) { return dot4(w.w, a.w, dot4(w.z, a.z, dot4(w.y, a.y, dot4(w.x, a.x, 0)))); }
 
 // Σ t[g] for g in 0..n, added in index order from +0. `t` is 16-byte aligned and readable up to n
-// rounded up to 4. Whole runs of 32 terms come in eight 128-bit reads, the next run in flight
-// while the current one is added (straight-line adds, no per-term branch); then the tail.
+// rounded up to 4. Whole runs of 32 terms come in eight 128-bit reads into two register sets in
+// turn: run c + 1's reads (clamped, never past the last run) go out before run c is added, so one
+// lane's chain of additions never waits for LDS (no copies between the sets, which would make the
+// additions wait for the reads in flight). Then the tail.
 __device__ __forceinline__ float ordered_sum(const float *t, int n)
 {
     constexpr int V = 8;  // 128-bit reads per run
     const v4f *t4 = reinterpret_cast<const v4f *>(t);
     const int runs = n / (4 * V);
     float s = 0.0f;
-    v4f cur[V], nxt[V];
-    if (runs > 0) {
+    v4f A[V], B[V];
+    auto load = [&](v4f *r, int c) {
 #pragma unroll
-        for (int k = 0; k < V; k++) cur[k] = t4[k];
-    }
-    for (int c = 0; c < runs; c++) {
-        if (c + 1 < runs) {
-#pragma unroll
-            for (int k = 0; k < V; k++) nxt[k] = t4[(c + 1) * V + k];
-        }
+        for (int k = 0; k < V; k++) r[k] = t4[c * V + k];
+    };
+    auto add = [&](const v4f *r) {
 #pragma unroll
         for (int k = 0; k < V; k++) {
-            s = s + cur[k].x;
-            s = s + cur[k].y;
-            s = s + cur[k].z;
-            s = s + cur[k].w;
+            s = s + r[k].x;
+            s = s + r[k].y;
+            s = s + r[k].z;
+            s = s + r[k].w;
         }
-#pragma unroll
-        for (int k = 0; k < V; k++) cur[k] = nxt[k];
+    };
+    if (runs > 0) {
+        load(A, 0);
+        for (int c = 0; c < runs; c += 2) {
+            load(B, min(c + 1, runs - 1));
+            __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the additions
+            add(A);
+            load(A, min(c + 2, runs - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 < runs) add(B);
+        }
     }
     const int g0 = runs * 4 * V, rest4 = (n - g0 + 3) / 4;  // uniform
     if (rest4 > 0) {
+        v4f cur[V];
 #pragma unroll
         for (int k = 0; k < V; k++) cur[k] = t4[runs * V + min(k, rest4 - 1)];
         // the row is zero-padded to whole float4s, and s is never -0 (it starts at +0), so the
@@ -322,28 +330,16 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         }
         float total;
         if (EXACT) {
-            v4f *row = reinterpret_cast<v4f *>(nbuf);
-            if (tid < n4) row[tid] = f[0];
-            if (tid + kThreads < n4) row[tid + kThreads] = f[1];
-            if (tid + 2 * kThreads < n4) row[tid + 2 * kThreads] = f[2];
-            if (tid + 3 * kThreads < n4) row[tid + 3 * kThreads] = f[3];
+            // dot_f32(row, row) in index order from −0 (arch/scalar.rs:340-342): the squares are
+            // formed by every thread, then one lane adds them with its reads running ahead (from
+            // +0: the squares are never −0, so the start's sign changes nothing)
+            v4f *sq = reinterpret_cast<v4f *>(nbuf);
+            if (tid < n4) sq[tid] = f[0] * f[0];
+            if (tid + kThreads < n4) sq[tid + kThreads] = f[1] * f[1];
+            if (tid + 2 * kThreads < n4) sq[tid + 2 * kThreads] = f[2] * f[2];
+            if (tid + 3 * kThreads < n4) sq[tid + 3 * kThreads] = f[3] * f[3];
             __syncthreads();
-            if (tid == 0) {
-                float s = -0.0f;  // dot_f32(row, row) in index order (arch/scalar.rs:340-342)
-                for (int i = 0; i < K; i += 32) {
-                    float4 f[8];
-#pragma unroll
-                    for (int k = 0; k < 8; k++) f[k] = *reinterpret_cast<const float4 *>(nbuf + i + 4 * k);
-#pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        s = s + f[k].x * f[k].x;
-                        s = s + f[k].y * f[k].y;
-                        s = s + f[k].z * f[k].z;
-                        s = s + f[k].w * f[k].w;
-                    }
-                }
-                red[4] = s;
-            }
+            if (tid == 0) red[4] = ordered_sum(nbuf, K);
             __syncthreads();
             total = red[4];
         } else {

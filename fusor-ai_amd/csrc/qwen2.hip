@@ -2,12 +2,12 @@
 // Prediction::predict (blocks/src/transformer.rs:185-341, layer.rs:161-344,
 // layer/input.rs:22-66, lm.rs:97-179), every projection through the projection kernel.
 //
-// Per layer, each projection with its neighbours fused in. In the reference's order (exact), six
+// Per layer, each projection with its neighbours fused in. In the reference's order (exact), five
 // launches:
 //   1. RMSNorm + quantize -> QKV product + bias -> RoPE on query/key heads, keys and values kept
-//   2. attention of every query head over the cache in two launches: the scores by key blocks,
-//      then softmax and weighted values by head and 32 value dimensions, quantized for the output
-//      projection
+//   2. attention of every query head over the cache, by head and 32 value dimensions: the scores,
+//      the softmax and the weighted values, quantized for the output projection (head sizes 64
+//      and 128; other sizes take two launches, the scores by key blocks and then the rest)
 //   3. output projection added to the residual row
 //   4. RMSNorm + quantize -> gate and up products -> silu(gate)·up, each workgroup's 32 outputs
 //      quantized as one group for down
@@ -264,6 +264,172 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
     }
 }
 
+// s + Σ t[j] for j in 0..n, added in index order by one lane; t 16-byte aligned. Runs of 16 (four 128-bit reads) into two register sets in turn, run c + 1's
+// reads (clamped, never past the last run) issued before run c is added, so the chain of
+// additions neither waits for LDS nor shares its issue slots with more than a read per four terms.
+__device__ __forceinline__ float chain_sum(float s, int n, const float *t)
+{
+    const v4f *t4 = reinterpret_cast<const v4f *>(t);
+    const int runs = n / 16;
+    v4f A[4], B[4];
+    auto load = [&](v4f *r, int c) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) r[e] = t4[c * 4 + e];
+    };
+    auto add = [&](const v4f *r) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            s = s + r[e].x;
+            s = s + r[e].y;
+            s = s + r[e].z;
+            s = s + r[e].w;
+        }
+    };
+    if (runs > 0) {
+        load(A, 0);
+        for (int c = 0; c < runs; c += 2) {
+            load(B, min(c + 1, runs - 1));
+            __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the additions
+            add(A);
+            load(A, min(c + 2, runs - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 1 < runs) add(B);
+        }
+    }
+    for (int j = runs * 16; j < n; j++) s = s + t[j];
+    return s;
+}
+
+// The exact-order attention of one query head for kWeighDims value dimensions in one launch (the
+// reference's arithmetic of attn_scores_kernel and attn_weigh_kernel<true>, ops.rs:301-342). Grid:
+// (heads, D / kWeighDims), 256 threads; every workgroup of a head forms the head's scores itself.
+//   scores: thread t takes keys j0 + t (two passes of 256 keys in flight at once when the rows
+//           fit in registers): dot_f32(q, k_j) from −0 in index order, times 1/√D;
+//   softmax: the maximum, w_j = ops::exp(s_j − max), their total from −0 in index order (one lane,
+//           reads running ahead of the additions: chain_sum), w_j / total;
+//   values: per chunk of 256 keys, thread t forms the 32 products w_j·v_j[i] of its key into LDS
+//           (a padded row per dimension), then lanes 0..31 of the first wave add their row to
+//           their output i in key order from +0,
+//           while every thread's loads of the next chunk are in flight. The value rows of the
+//           first two chunks are requested before the scores, so their latency hides under them.
+// Then the 32 outputs are quantized as one group for the output projection.
+constexpr int kExactChunk = 256;
+constexpr int kProdRow = kExactChunk + 4;  // one dimension's products over a chunk, padded: the
+                                          // lanes' 128-bit reads of their rows spread over the banks
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
+{
+    extern __shared__ __align__(16) float ash[];
+    constexpr int D4 = D / 4, PASS = D <= 64 ? 2 : 1;  // key rows in registers per thread
+    const int keys = a.keys, tid = threadIdx.x;
+    const int head = blockIdx.x, d0 = int(blockIdx.y) * kWeighDims;
+    const int kv = head / (a.heads / a.kv_heads);
+    float *qs = ash;                                     // [D] the rotated query
+    float *w = qs + D;                                   // [capacity] scores, then weights
+    float *prod = w + (a.capacity + 15) / 16 * 16;       // [kWeighDims][kProdRow] products
+    float *red = prod + kWeighDims * kProdRow;           // [16]
+    const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
+    const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D + d0;
+    // this thread's value row in chunk c (clamped re-reads past the end)
+    auto fetch_row = [&](int c, v4f *r) {
+#pragma unroll
+        for (int e = 0; e < kWeighDims / 4; e++)
+            r[e] = *reinterpret_cast<const v4f *>(vbase + size_t(min(c * kExactChunk + tid, keys - 1)) * D + 4 * e);
+    };
+    // the value rows of the first two chunks, requested before the scores
+    v4f va[kWeighDims / 4], vb[kWeighDims / 4];
+    fetch_row(0, va);
+    fetch_row(1, vb);
+    if (tid < D4) reinterpret_cast<v4f *>(qs)[tid] = reinterpret_cast<const v4f *>(a.qkv + size_t(head) * D)[tid];
+    const float scale = 1.0f / sqrtf(float(D));
+    float local_max = -INFINITY;
+    for (int j0 = 0; j0 < keys; j0 += PASS * kExactChunk) {
+        v4f kr[PASS][D4];
+#pragma unroll
+        for (int u = 0; u < PASS; u++)
+#pragma unroll
+            for (int e = 0; e < D4; e++)
+                kr[u][e] = *reinterpret_cast<const v4f *>(kbase + size_t(min(j0 + u * kExactChunk + tid, keys - 1)) * D + 4 * e);
+        __syncthreads();  // the query (first pass)
+#pragma unroll
+        for (int u = 0; u < PASS; u++) {
+            const int j = j0 + u * kExactChunk + tid;
+            float s = -0.0f;  // dot_f32 in index order (arch/scalar.rs:340-342)
+#pragma unroll
+            for (int e = 0; e < D4; e++) {
+                const v4f qv = reinterpret_cast<const v4f *>(qs)[e];
+                s = s + qv.x * kr[u][e].x;
+                s = s + qv.y * kr[u][e].y;
+                s = s + qv.z * kr[u][e].z;
+                s = s + qv.w * kr[u][e].w;
+            }
+            if (j < keys) {
+                w[j] = s * scale;
+                local_max = fmaxf(local_max, s * scale);
+            }
+        }
+    }
+    const float peak = attn_block_max(local_max, red);  // its barriers publish the scores
+    for (int j = tid; j < keys; j += kAttnThreads) w[j] = ref_exp(w[j] - peak);
+    __syncthreads();
+    // the exponentials summed in index order by one lane
+    if (tid == 0) red[8] = chain_sum(-0.0f, keys, w);
+    __syncthreads();
+    const float total = red[8];
+    for (int j = tid; j < keys; j += kAttnThreads) w[j] = w[j] / total;
+    float o = 0.0f;  // lanes 0..31 of wave 0: output d0 + lane
+    // Chunk c from the registers `v`: its products into LDS, then (lanes 0..31) their ordered
+    // sums, while `v` is refilled with chunk c + 2.
+    auto chunk = [&](int c, v4f *v) {
+        const int j0 = c * kExactChunk, n = min(kExactChunk, keys - j0);
+        __syncthreads();  // the weights (first chunk); the previous chunk's products all added
+        {
+            const float wj = tid < n ? w[j0 + tid] : 0.0f;
+            float *col = prod + tid;
+#pragma unroll
+            for (int e = 0; e < kWeighDims / 4; e++) {
+                col[(4 * e) * kProdRow] = wj * v[e].x;
+                col[(4 * e + 1) * kProdRow] = wj * v[e].y;
+                col[(4 * e + 2) * kProdRow] = wj * v[e].z;
+                col[(4 * e + 3) * kProdRow] = wj * v[e].w;
+            }
+        }
+        __syncthreads();
+        if (j0 + 2 * kExactChunk < keys) fetch_row(c + 2, v);
+        if (tid < kWeighDims) o = chain_sum(o, n, prod + tid * kProdRow);
+    };
+    for (int c = 0; c * kExactChunk < keys; c += 2) {
+        chunk(c, va);
+        if ((c + 1) * kExactChunk < keys) chunk(c + 1, vb);
+    }
+    // the 32 outputs quantized as one group (eight lanes, four values each)
+    __syncthreads();
+    if (tid < kWeighDims) prod[tid] = o;
+    __syncthreads();
+    const int sub = tid & 7;
+    if (tid < 8) {
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = prod[sub * 4 + e];
+        if (a.row_out) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) a.row_out[head * D + d0 + sub * 4 + e] = x[e];
+        }
+        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        amax = max8(fmaxf(0.0f, amax));
+        int l0, l1, l2, l3;
+        const float d = scale_and_levels(amax, x[0], x[1], x[2], x[3], l0, l1, l2, l3);
+        const int sum = sum8(l0 + l1 + l2 + l3);
+        const int G = (head * D + d0) / 32;
+        reinterpret_cast<int *>(a.q)[G * 8 + sub] = pack4(l0, l1, l2, l3);
+        if (sub == 0) {
+            a.scales[G] = d;
+            a.corr[G] = -a.zp * sum;
+        }
+    }
+}
+
 // Prediction::greedy (lm.rs:169-179) over the head's per-workgroup candidates: the first index of
 // the largest logit; NaNs never win, and a NaN first logit keeps index 0.
 __global__ __launch_bounds__(1024) void greedy_kernel(const float *__restrict__ pval, const int32_t *__restrict__ pidx, int n,
@@ -323,7 +489,7 @@ struct fg_qwen2 {
     float *scores;     // [heads][capacity]
     float *part;       // fast attention: [heads][chunks][D + 4]
     int chunks, per_chunk;
-    size_t score_smem, weigh_smem;
+    size_t score_smem, weigh_smem, exact_smem;
     int zp;
 };
 
@@ -489,10 +655,18 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st, fl
     a.scales = m->xs;
     a.corr = m->xc;
     a.row_out = row_out;
+    const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims));
+    if (sh.exact && (sh.head_dim == 64 || sh.head_dim == 128)) {
+        // one launch: the head's scores, softmax and ordered weighted sums (measured faster than
+        // the scores kernel followed by this kernel's softmax and sums alone)
+        if (sh.head_dim == 64) attn_exact_kernel<64><<<wgrid, kAttnThreads, m->exact_smem, st>>>(a);
+        else attn_exact_kernel<128><<<wgrid, kAttnThreads, m->exact_smem, st>>>(a);
+        FG_HIP(hipGetLastError());
+        return FG_OK;
+    }
     const dim3 sgrid(unsigned(sh.kv_heads), unsigned((a.keys + kScoreKeys - 1) / kScoreKeys));
     attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
     FG_HIP(hipGetLastError());
-    const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims));
     if (sh.exact) attn_weigh_kernel<true><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
     else attn_weigh_kernel<false><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
     FG_HIP(hipGetLastError());
@@ -579,7 +753,9 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
     const int group = int(sh.heads / sh.kv_heads);
     m->score_smem = size_t(kScoreKeys * (D + 1) + group * D) * 4;
     m->weigh_smem = size_t(kWeighKeys * (kWeighDims + 1) + sh.capacity + 8 * kWeighDims + 16) * 4;
-    if (group * D > 4 * kAttnThreads || m->score_smem > 64 * 1024 || m->weigh_smem > 64 * 1024) {
+    m->exact_smem = size_t(D + (sh.capacity + 15) / 16 * 16 + kWeighDims * kProdRow + 16) * 4;
+    if (group * D > 4 * kAttnThreads || m->score_smem > 64 * 1024 || m->weigh_smem > 64 * 1024 ||
+        m->exact_smem > 64 * 1024) {
         delete m;
         return set_error(FG_ERR_SHAPE, "fg_qwen2_create: the attention does not fit (heads per KV head x head_dim <= 1024, capacity)");
     }

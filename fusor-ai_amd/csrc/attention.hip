@@ -180,11 +180,14 @@ __global__ void value_table_kernel(const float *__restrict__ value, size_t strid
 
 // The queries of every (image, head), quantized as the product quantizes its rows (quantize_rows,
 // matmul.rs:233-257, for a Q7b32 matrix: zero point 64) over the padded width pd, zeros past
-// head_dim: levels [u][r][pd], scales and corrections [u][r][pd / 32]. Eight lanes per group of 32.
+// head_dim: levels [u][r][pd], scales and corrections [u][r][pd / 32], and when `tscales` is set
+// the scales block-major as well, [u][pd / 32][queries] (the form the scores' product reads).
+// Eight lanes per group of 32.
 __global__ __launch_bounds__(256) void query_levels_kernel(const float *__restrict__ query, size_t stride,
                                                            size_t offset, int heads, int queries, int hd, int pd,
                                                            size_t slots, int8_t *__restrict__ levels,
-                                                           float *__restrict__ lscales, int32_t *__restrict__ lcorr)
+                                                           float *__restrict__ lscales, int32_t *__restrict__ lcorr,
+                                                           float *__restrict__ tscales)
 {
     const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int per_row = pd / 4;
@@ -201,6 +204,7 @@ __global__ __launch_bounds__(256) void query_levels_kernel(const float *__restri
     Group8 gr[1];
     quantize_groups<1>(&v, gr);
     if (active) store_group8(gr[0], 64, s4 / 8, levels + rr * pd, lscales + rr * (pd / 32), lcorr + rr * (pd / 32));
+    if (tscales && active && (threadIdx.x & 7) == 0) tscales[(u * (pd / 32) + s4 / 8) * size_t(queries) + r] = gr[0].d;
 }
 
 // One workgroup of four waves per query row: the row's scores (product · scale below keys4,
@@ -362,7 +366,7 @@ struct Shape {
 // of every (image, key head) and the quantized queries of every (image, head) are built up front;
 // the scores, their levels and the products' outputs are per head.
 struct Scratch {
-    enum { KEYT, MEAN, KCODES, KSCALES, VCODES, VSCALES, QLEVELS, QSCALES, QCORR, PROD, ELEVELS, ESCALES, ECORR, SUMS, PV, N };
+    enum { KEYT, MEAN, KCODES, KSCALES, VCODES, VSCALES, QLEVELS, QSCALES, QCORR, QTSCALES, PROD, ELEVELS, ESCALES, ECORR, SUMS, PV, N };
     size_t size[N];
     void *part[N];
     explicit Scratch(const Shape &s)
@@ -375,6 +379,7 @@ struct Scratch {
         size[VSCALES] = s.ktables * s.vquads * (s.pk / 32) * 16;
         size[QLEVELS] = s.qtables * s.queries * s.pd;
         size[QSCALES] = size[QCORR] = s.qtables * s.queries * (s.pd / 32) * 4;
+        size[QTSCALES] = s.queries % 128 == 0 ? size[QSCALES] : 0;  // block-major, whole tiles of rows only
         size[PROD] = s.queries * s.keys4 * 4;
         size[ELEVELS] = s.queries * s.pk;
         size[ESCALES] = size[ECORR] = s.queries * (s.pk / 32) * 4;
@@ -421,7 +426,8 @@ int run(const fg_attention *c, float *out, hipStream_t st, const Shape &s, const
     const size_t slots = s.qtables * s.queries * (s.pd / 4);
     query_levels_kernel<<<blocks_for(slots), kThreads, 0, st>>>(
         c->query, c->query_stride, c->query_offset, int(c->heads), queries, hd, pd, slots,
-        w.at<int8_t>(Scratch::QLEVELS), w.at<float>(Scratch::QSCALES), w.at<int32_t>(Scratch::QCORR));
+        w.at<int8_t>(Scratch::QLEVELS), w.at<float>(Scratch::QSCALES), w.at<int32_t>(Scratch::QCORR),
+        s.queries % 128 == 0 ? w.at<float>(Scratch::QTSCALES) : nullptr);
     FG_HIP(hipGetLastError());
     int rc;
     for (size_t image = 0; image < c->images; image++) {
@@ -439,6 +445,10 @@ int run(const fg_attention *c, float *out, hipStream_t st, const Shape &s, const
                 a.q = w.at<int8_t>(Scratch::QLEVELS) + u * s.queries * s.pd;
                 a.as = w.at<float>(Scratch::QSCALES) + u * s.queries * (s.pd / 32);
                 a.corr = w.at<int32_t>(Scratch::QCORR) + u * s.queries * (s.pd / 32);
+                if (s.queries % 128 == 0) {
+                    a.as_t = w.at<float>(Scratch::QTSCALES) + u * s.queries * (s.pd / 32);
+                    a.as_t_rows = s.queries;
+                }
                 a.rows = s.queries;
                 a.quad_begin = 0;
                 a.quad_end = size_t(keys4 / 4);

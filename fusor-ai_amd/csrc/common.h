@@ -324,6 +324,10 @@ int table_alloc(int dtype, size_t rows, size_t cols, fg_table **out);
 size_t table_byte_len(int dtype, size_t rows, size_t cols);
 int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint8_t *bytes, hipStream_t s);
 int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s);
+// quantize_rows for groups of 32 with the scales written block-major, as_t[g][Mpad] (zeros for the
+// rows past `rows`), and no corrections: the form the batched product's kernels read.
+int launch_quantize_rows_t(const float *x, size_t rows, size_t K, int dtype, int8_t *q, float *as_t, size_t Mpad,
+                           hipStream_t s);
 int launch_quantize_rows(const float *x, size_t count, int dtype, int8_t *q, float *scales, int32_t *corr,
                          hipStream_t s);
 int launch_qmatrix_clear(fg_table *t, size_t first, size_t last, hipStream_t s);
@@ -350,6 +354,10 @@ struct ProductArgs {
     // allocated or freed; a product that needs more than `workspace_bytes` fails
     void *workspace;
     size_t workspace_bytes;
+    // pre-quantized rows may bring their scales block-major as well ([G][as_t_rows], rows past
+    // `rows` zero): a kernel that reads that form takes it instead of a transposed copy
+    const float *as_t;
+    size_t as_t_rows;
 };
 // Scratch bytes a product needs beyond its inputs and outputs (0 for the matrix-vector rows).
 size_t product_scratch_bytes(const ProductArgs &a);

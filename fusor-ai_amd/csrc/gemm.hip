@@ -1210,20 +1210,27 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
     const float *as = a.as;
     char *base = static_cast<char *>(ws);
     int rc = FG_OK;
+    float *as_t = reinterpret_cast<float *>(base + q_bytes + 2 * s_bytes);
+    // the kernels that read block-major scales read only them: f32 rows are quantized straight
+    // into that form, and pre-quantized rows that bring it are not transposed again
+    const bool caller_t = !a.x && a.as_t && a.as_t_rows == size_t(Mpad);
     if (a.x) {
         q = reinterpret_cast<int8_t *>(base);
-        float *sc = reinterpret_cast<float *>(base + q_bytes);
-        int32_t *co = reinterpret_cast<int32_t *>(base + q_bytes + s_bytes);
-        rc = launch_quantize_rows(a.x, size_t(M) * K, t->dtype, q, sc, co, s);
-        as = sc;
-    }
-    float *as_t = reinterpret_cast<float *>(base + q_bytes + 2 * s_bytes);
-    if (rc == FG_OK && t_bytes) {
+        if (t_bytes) {
+            rc = launch_quantize_rows_t(a.x, size_t(M), size_t(K), t->dtype, q, as_t, size_t(Mpad), s);
+        } else {
+            float *sc = reinterpret_cast<float *>(base + q_bytes);
+            int32_t *co = reinterpret_cast<int32_t *>(base + q_bytes + s_bytes);
+            rc = launch_quantize_rows(a.x, size_t(M) * K, t->dtype, q, sc, co, s);
+            as = sc;
+        }
+    } else if (t_bytes && !caller_t) {
         const size_t n = size_t(G) * Mpad;
         transpose_scales_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(as, M, G, Mpad, as_t);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) rc = check_hip(e, "transpose_scales_kernel");
     }
+    const float *as_block = caller_t && t_bytes ? a.as_t : as_t;
     if (rc == FG_OK) {
         GemmParams p{};
         p.codes = t->codes;
@@ -1238,7 +1245,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         p.n_rows = int(t->rows);
         p.q = q;
         p.as = as;
-        p.as_t = as_t;
+        p.as_t = as_block;
         p.bias = a.bias;
         p.out = a.out;
         p.ld_out = long(a.ld_out);

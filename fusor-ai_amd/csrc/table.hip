@@ -295,6 +295,44 @@ int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t
     return FG_OK;
 }
 
+namespace {
+
+// quantize_rows_kernel<8>'s arithmetic for groups of 32, the scale of group g of row r stored at
+// as_t[g·Mpad + r]; the slots of rows rows..Mpad-1 get zero scales.
+__global__ void quantize_rows_t_kernel(const float *__restrict__ x, size_t groups, int G, size_t Mpad, int8_t *__restrict__ q,
+                                       float *__restrict__ as_t)
+{
+    const size_t t = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t g = t / 8;
+    const int sub = int(t % 8);
+    const bool active = g < groups;
+    const float4 v = active ? reinterpret_cast<const float4 *>(x)[g * 8 + sub] : make_float4(0, 0, 0, 0);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = max8(fmaxf(0.0f, amax));
+    int l0, l1, l2, l3;
+    const float d = scale_and_levels(amax, v.x, v.y, v.z, v.w, l0, l1, l2, l3);
+    const size_t r = g / G, gi = g % G;
+    if (active) {
+        reinterpret_cast<int *>(q)[g * 8 + sub] = pack4(l0, l1, l2, l3);
+        if (sub == 0) as_t[gi * Mpad + r] = d;
+    } else if (r < Mpad && sub == 0) {
+        as_t[gi * Mpad + r] = 0.0f;
+    }
+}
+
+}  // namespace
+
+int launch_quantize_rows_t(const float *x, size_t rows, size_t K, int dtype, int8_t *q, float *as_t, size_t Mpad,
+                           hipStream_t s)
+{
+    if (group_of(dtype) != 32) return set_error(FG_ERR_FORMAT, "block-major scales take groups of 32");
+    const size_t G = K / 32, groups = rows * G, threads = Mpad * G * 8;
+    if (threads == 0) return FG_OK;
+    quantize_rows_t_kernel<<<unsigned((threads + 255) / 256), 256, 0, s>>>(x, groups, int(G), Mpad, q, as_t);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
 int launch_quantize_rows(const float *x, size_t count, int dtype, int8_t *q, float *scales, int32_t *corr,
                          hipStream_t s)
 {

@@ -207,13 +207,17 @@ __global__ __launch_bounds__(256) void query_levels_kernel(const float *__restri
     if (tscales && active && (threadIdx.x & 7) == 0) tscales[(u * (pd / 32) + s4 / 8) * size_t(queries) + r] = gr[0].d;
 }
 
-// One workgroup of four waves per query row: the row's scores (product · scale below keys4,
-// zeros to pk) staged in LDS, their maximum over the first `keys`, the exponentials there (all
-// 256 threads), then two things at once: the first wave sums the exponentials in the scalar
-// backend's order (scalar.rs:117-126, ops.rs:170-175: lane o < 8 sums offset o over the whole
-// runs of eight in order, lane 0 adds the rest in order, then the eight offset sums in order),
-// and the other three quantize the row for the product with the values.
-template <bool FAST>
+// One workgroup of four waves per query row; thread t holds slots t, t + 256, ... (S of them, four
+// scores each) in registers: the row's scores (product · scale below keys4, zeros to pk), their
+// maximum over the first `keys`, the exponentials there, and the row quantized straight from
+// the registers for the product with the values (quantize_rows over the whole padded width for a
+// Q7b32 matrix, zero point 64: eight consecutive slots are eight aligned lanes, and the S groups
+// of a thread are independent streams the scheduler interleaves). The exponentials also go to
+// LDS, where after one barrier lanes 0..7 of the first wave sum them in the scalar backend's order
+// (scalar.rs:117-126, ops.rs:170-175): lane o sums offset o over the whole runs of eight in
+// order, lane 0 adds the rest in order, then the eight offset sums in order. Per-element bounds
+// are selects, not branches.
+template <bool FAST, int S>
 __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restrict__ prod, int keys4, float scale,
                                                            int keys, int pk, int8_t *__restrict__ levels,
                                                            float *__restrict__ level_scales, int32_t *__restrict__ level_corr,
@@ -226,42 +230,48 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
     const size_t r = blockIdx.x;
     const int n4 = pk / 4, k4 = keys4 / 4;
     const v4f *src = reinterpret_cast<const v4f *>(prod + r * keys4);
+    v4f v[S];
+#pragma unroll
+    for (int k = 0; k < S; k++) v[k] = src[min(tid + 256 * k, k4 - 1)];
     float m = -INFINITY;
-    for (int s0 = 0; s0 < n4; s0 += 1024) {
-        v4f v[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int slot = s0 + 256 * u + tid;
-            v[u] = slot < k4 ? src[slot] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int slot = s0 + 256 * u + tid;
-            if (slot < n4) {
-                const v4f x{v[u].x * scale, v[u].y * scale, v[u].z * scale, v[u].w * scale};
-                row4[slot] = x;
-                const int i = 4 * slot;
-                if (i < keys) m = fmaxf(m, x.x);
-                if (i + 1 < keys) m = fmaxf(m, x.y);
-                if (i + 2 < keys) m = fmaxf(m, x.z);
-                if (i + 3 < keys) m = fmaxf(m, x.w);
-            }
-        }
+    for (int k = 0; k < S; k++) {
+        const int slot = tid + 256 * k, i = 4 * slot;
+        const v4f x = slot < k4 ? v4f{v[k].x * scale, v[k].y * scale, v[k].z * scale, v[k].w * scale}
+                                : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        v[k] = x;
+        m = fmaxf(m, i < keys ? x.x : -INFINITY);
+        m = fmaxf(m, i + 1 < keys ? x.y : -INFINITY);
+        m = fmaxf(m, i + 2 < keys ? x.z : -INFINITY);
+        m = fmaxf(m, i + 3 < keys ? x.w : -INFINITY);
     }
     for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
     if (lane == 0) wmax[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    for (int slot = tid; 4 * slot < keys; slot += 256) {
-        v4f x = row4[slot];
-        const int i = 4 * slot;
-        x.x = FAST ? ref_exp_fast(x.x - m) : ref_exp(x.x - m);
-        if (i + 1 < keys) x.y = FAST ? ref_exp_fast(x.y - m) : ref_exp(x.y - m);
-        if (i + 2 < keys) x.z = FAST ? ref_exp_fast(x.z - m) : ref_exp(x.z - m);
-        if (i + 3 < keys) x.w = FAST ? ref_exp_fast(x.w - m) : ref_exp(x.w - m);
-        row4[slot] = x;
+#pragma unroll
+    for (int k = 0; k < S; k++) {
+        const int slot = tid + 256 * k, i = 4 * slot;
+        v4f e = v[k];
+        const float ex = FAST ? ref_exp_fast(e.x - m) : ref_exp(e.x - m);
+        const float ey = FAST ? ref_exp_fast(e.y - m) : ref_exp(e.y - m);
+        const float ez = FAST ? ref_exp_fast(e.z - m) : ref_exp(e.z - m);
+        const float ew = FAST ? ref_exp_fast(e.w - m) : ref_exp(e.w - m);
+        e.x = i < keys ? ex : e.x;
+        e.y = i + 1 < keys ? ey : e.y;
+        e.z = i + 2 < keys ? ez : e.z;
+        e.w = i + 3 < keys ? ew : e.w;
+        v[k] = e;
+        if (slot < n4) row4[slot] = e;
     }
-    __syncthreads();
+    Group8 gr[S];
+    quantize_groups<S>(v, gr);
+#pragma unroll
+    for (int k = 0; k < S; k++) {
+        const int slot = tid + 256 * k;
+        if (slot < n4) store_group8(gr[k], 64, slot / 8, levels + r * pk, level_scales + r * (pk / 32), level_corr + r * (pk / 32));
+    }
+    __syncthreads();  // the exponentials in LDS
     if (wave == 0) {
         const int whole = keys / 8 * 8;
         float part = 0.0f;
@@ -269,11 +279,11 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
             // sixteen reads out before their sixteen additions, in run order
             int i = lane;
             for (; i + 8 * 15 < whole; i += 8 * 16) {
-                float v[16];
+                float x[16];
 #pragma unroll
-                for (int u = 0; u < 16; u++) v[u] = row[i + 8 * u];
+                for (int u = 0; u < 16; u++) x[u] = row[i + 8 * u];
 #pragma unroll
-                for (int u = 0; u < 16; u++) part = part + v[u];
+                for (int u = 0; u < 16; u++) part = part + x[u];
             }
             for (; i < whole; i += 8) part = part + row[i];
         }
@@ -287,17 +297,6 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
             if (lane == 0) total = total + po;
         }
         if (lane == 0) sums[r] = total;
-        return;
-    }
-    // The row, as the product with the values takes it: quantize_rows over its whole padded width
-    // for a Q7b32 matrix (zero point 64), eight lanes per group of 32, by the three other waves
-    // (slot ≡ thread mod 8, so each group of eight slots is eight aligned lanes of one wave).
-    for (int s0 = 0; s0 < n4; s0 += 192) {
-        const int slot = s0 + tid - 64;
-        const v4f v[1] = {slot < n4 ? row4[slot] : v4f{0.0f, 0.0f, 0.0f, 0.0f}};
-        Group8 gr[1];
-        quantize_groups<1>(v, gr);
-        if (slot < n4) store_group8(gr[0], 64, slot / 8, levels + r * pk, level_scales + r * (pk / 32), level_corr + r * (pk / 32));
     }
 }
 
@@ -317,17 +316,30 @@ unsigned blocks_for(size_t n) { return unsigned((n + kThreads - 1) / kThreads); 
 
 // A query row per workgroup; a row of 16384 keys takes 64 KiB and 16 bytes of LDS, past the
 // default limit, which is then raised for the kernel on the current device.
+template <bool FAST, int S>
+int launch_exponentials_s(const float *prod, int keys4, float scale, int keys, int pk, int8_t *levels, float *level_scales,
+                          int32_t *level_corr, float *sums, unsigned queries, hipStream_t st)
+{
+    const size_t smem = size_t(pk) * 4 + 16;
+    if (smem > 64 * 1024)
+        FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(exponentials_kernel<FAST, S>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    exponentials_kernel<FAST, S><<<queries, 256, smem, st>>>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+// Slots per thread: the fewest powers of two whose 256 threads cover the row's pk / 4 slots.
 template <bool FAST>
 int launch_exponentials(const float *prod, int keys4, float scale, int keys, int pk, int8_t *levels, float *level_scales,
                         int32_t *level_corr, float *sums, unsigned queries, hipStream_t st)
 {
-    const size_t smem = size_t(pk) * 4 + 16;
-    if (smem > 64 * 1024)
-        FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(exponentials_kernel<FAST>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    exponentials_kernel<FAST><<<queries, 256, smem, st>>>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums);
-    FG_HIP(hipGetLastError());
-    return FG_OK;
+    const int slots = (pk / 4 + 255) / 256;
+    if (slots <= 1) return launch_exponentials_s<FAST, 1>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums, queries, st);
+    if (slots <= 2) return launch_exponentials_s<FAST, 2>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums, queries, st);
+    if (slots <= 4) return launch_exponentials_s<FAST, 4>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums, queries, st);
+    if (slots <= 8) return launch_exponentials_s<FAST, 8>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums, queries, st);
+    return launch_exponentials_s<FAST, 16>(prod, keys4, scale, keys, pk, levels, level_scales, level_corr, sums, queries, st);
 }
 
 // A run-time Q7b32 matrix (QuantizedMatrix) over caller-provided device storage: `rows` rows of

@@ -264,21 +264,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
     }
 }
 
-// s + Σ t[j] for j in 0..n, added in index order by one lane; t 16-byte aligned. Runs of 16 (four 128-bit reads) into two register sets in turn, run c + 1's
-// reads (clamped, never past the last run) issued before run c is added, so the chain of
-// additions neither waits for LDS nor shares its issue slots with more than a read per four terms.
+// s + Σ t[j] for j in 0..n, added in index order by one lane; t 16-byte aligned. Runs of 32 (eight
+// 128-bit reads) into two register sets in turn, run c + 1's reads (clamped, never past the last
+// run) issued before run c is added: 32 dependent additions outlast an LDS read, so the chain
+// neither waits for LDS nor shares its issue slots with more than a read per four terms.
 __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
 {
+    constexpr int V = 8;  // 128-bit reads per run
     const v4f *t4 = reinterpret_cast<const v4f *>(t);
-    const int runs = n / 16;
-    v4f A[4], B[4];
+    const int runs = n / (4 * V);
+    v4f A[V], B[V];
     auto load = [&](v4f *r, int c) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) r[e] = t4[c * 4 + e];
+        for (int e = 0; e < V; e++) r[e] = t4[c * V + e];
     };
     auto add = [&](const v4f *r) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
+        for (int e = 0; e < V; e++) {
             s = s + r[e].x;
             s = s + r[e].y;
             s = s + r[e].z;
@@ -296,7 +298,7 @@ __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
             if (c + 1 < runs) add(B);
         }
     }
-    for (int j = runs * 16; j < n; j++) s = s + t[j];
+    for (int j = runs * 4 * V; j < n; j++) s = s + t[j];
     return s;
 }
 

@@ -393,6 +393,20 @@ def test_int4_shape_bit_exact(fk, rows):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+@pytest.mark.parametrize("rows,k", [(5, 32 * 8), (16, 32 * 8), (9, 32 * 17)])
+def test_small_batch_streamed_with_one_or_two_stages(fk, dtype, rows, k):
+    """The streamed small-batch product with fewer blocks than one stage of 16 (8 blocks), and one
+    whole stage and a single block of a second (17 blocks); 5-16 rows, 8228 columns."""
+    n = 8228
+    data = synthetic_table(dtype, n, k, seed=rows + k)
+    t = table(fk, dtype, n, k, data)
+    x = activations(rows, k, seed=rows * 7 + k, outliers=0.02)
+    got = gpu_product(fk, t, x, rows)
+    want = oracle_product(dtype, n, k, data, x, rows)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
 @pytest.mark.parametrize("rows", [5, 16])
 def test_small_batch_streamed_over_many_columns(fk, dtype, rows):

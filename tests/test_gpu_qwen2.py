@@ -142,6 +142,22 @@ def test_decoder_head_sizes_and_many_key_chunks(fk, head_dim, heads, kv_heads):
         assert rel_l2(got[1], want[1]) < FAST_TOLERANCE, ("fast logits", position)
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(64, 4, 2), (128, 2, 1)])
+def test_exact_attention_with_few_keys_and_a_ragged_capacity(fk, head_dim, heads, kv_heads):
+    """The one-launch exact-order attention (head sizes 64 and 128) with 1, 2, 16, 17 and 37 keys in
+    a cache of 37 positions (its LDS rows are laid out past a capacity that is not whole runs of
+    16): bit-identical to the oracle's step."""
+    shape = dict(hidden=128, layers=2, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=256, vocab=64,
+                 capacity=37)
+    params = build(O.Q7B32, seed=head_dim + 1, synthetic=False, **shape)
+    for position in (0, 1, 15, 16, 36):
+        got, want = run_both(fk, O.Q7B32, params, token=5, position=position, exact=True)
+        assert same_bits(got[0], want[0]), ("hidden", position)
+        assert same_bits(got[1], want[1]), ("logits", position)
+        assert got[2] == want[2]
+        assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+
+
 def test_decoder_with_rows_of_heads_wider_than_1024(fk):
     """12 query heads of 128 over 2 key heads: the attention row (1536) is past what the
     flash-decoding merge takes, so parallel order runs the scores and weighted-sum kernels with

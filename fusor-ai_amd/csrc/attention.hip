@@ -514,6 +514,10 @@ extern "C" int fg_attend(const fg_attention *c, float *out, void *stream)
     if (c->exponentials != FG_EXP_EXACT && c->exponentials != FG_EXP_FAST)
         return set_error(FG_ERR_ARG, "fg_attend: exponentials must be FG_EXP_EXACT or FG_EXP_FAST");
     if (pad32(c->keys) * 4 > size_t(kMaxRowBytes)) return set_error(FG_ERR_SHAPE, "fg_attend: at most 16384 keys");
+    // the keys' transpose takes one grid layer per (image, key head); the row kernels a workgroup
+    // per query row
+    if (c->images * c->kv_heads > 65535 || c->queries > 0x7fffffff)
+        return set_error(FG_ERR_SHAPE, "fg_attend: at most 65535 images x key heads and 2^31 - 1 queries");
     // every head of a row lies within the row's stride
     if (c->query_offset + c->heads * c->head_dim > c->query_stride ||
         c->key_offset + c->kv_heads * c->head_dim > c->key_stride ||

@@ -305,73 +305,134 @@ __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
 // The exact-order attention of one query head for kWeighDims value dimensions in one launch (the
 // reference's arithmetic of attn_scores_kernel and attn_weigh_kernel<true>, ops.rs:301-342). Grid:
 // (heads, D / kWeighDims), 256 threads; every workgroup of a head forms the head's scores itself.
-//   scores: thread t takes keys j0 + t (two passes of 256 keys in flight at once when the rows
-//           fit in registers): dot_f32(q, k_j) from −0 in index order, times 1/√D;
+// Every load is coalesced: neighbouring lanes read neighbouring 16 bytes of one key (or value)
+// row, and the rows' products reach the lane that adds them through LDS.
+//   scores: a wave takes a batch of 16·KPI keys (KPI = 256 / D rows per load), lane l holding
+//           piece l % (D/4) of rows l / (D/4) + KPI·e; it forms the products q·k of its pieces into
+//           its wave's LDS stage (row-major, each row's pieces rotated by the row so that the reads
+//           below spread over the banks), and lane r then adds row r's D products in index order
+//           from −0 (dot_f32), times 1/√D. Two batches per wave are in flight;
 //   softmax: the maximum, w_j = ops::exp(s_j − max), their total from −0 in index order (one lane,
 //           reads running ahead of the additions: chain_sum), w_j / total;
-//   values: per chunk of 256 keys, thread t forms the 32 products w_j·v_j[i] of its key into LDS
-//           (a padded row per dimension), then lanes 0..31 of the first wave add their row to
-//           their output i in key order from +0,
-//           while every thread's loads of the next chunk are in flight. The value rows of the
-//           first two chunks are requested before the scores, so their latency hides under them.
+//   values: per chunk of 256 keys, lane l of a wave holds piece l % 8 (four dimensions) of rows
+//           l / 8 + 8·e and forms their products w_j·v_j[i] into LDS (a padded row per
+//           dimension, two buffers); lanes 0..31 of the first wave add their row to their output
+//           i in key order from +0 while the other waves form the next chunk's products. The
+//           value rows of the first two chunks are requested when the scores are done, so their
+//           latency hides under the softmax.
 // Then the 32 outputs are quantized as one group for the output projection.
 constexpr int kExactChunk = 256;
 constexpr int kProdRow = kExactChunk + 4;  // one dimension's products over a chunk, padded: the
                                           // lanes' 128-bit reads of their rows spread over the banks
+constexpr int kExactStage = 16384;         // bytes of one wave's batch of score products
+// the region after the weights: the four waves' score stages, then two buffers of value products
+constexpr int kExactRegion = 2 * kWeighDims * kProdRow * 4;
+static_assert(4 * kExactStage <= kExactRegion, "exact region");
+
+inline size_t exact_attention_smem(size_t capacity) { return size_t((capacity + 15) / 16 * 16 + 16) * 4 + kExactRegion; }
 
 template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
 {
     extern __shared__ __align__(16) float ash[];
-    constexpr int D4 = D / 4, PASS = D <= 64 ? 2 : 1;  // key rows in registers per thread
-    const int keys = a.keys, tid = threadIdx.x;
+    constexpr int PPL = D / 4;       // 16-byte pieces per key row
+    constexpr int KPI = 64 / PPL;    // key rows per wave load
+    constexpr int NI = 16;           // loads per batch
+    constexpr int BATCH = NI * KPI;  // keys per wave and batch (64 for D = 64, 32 for D = 128)
+    constexpr int STEP = 4 * BATCH;  // keys per workgroup and batch
+    static_assert(BATCH * D * 4 == kExactStage, "exact stage");
+    const int keys = a.keys, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int head = blockIdx.x, d0 = int(blockIdx.y) * kWeighDims;
     const int kv = head / (a.heads / a.kv_heads);
-    float *qs = ash;                                     // [D] the rotated query
-    float *w = qs + D;                                   // [capacity] scores, then weights
-    float *prod = w + (a.capacity + 15) / 16 * 16;       // [kWeighDims][kProdRow] products
-    float *red = prod + kWeighDims * kProdRow;           // [16]
+    float *w = ash;                                     // [capacity] scores, then weights
+    float *red = w + (a.capacity + 15) / 16 * 16;       // [16]
+    float *stage = red + 16 + wave * (BATCH * D);       // this wave's [BATCH][D] score products
+    float *prod = red + 16;                             // [2][kWeighDims][kProdRow] value products
     const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
     const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D + d0;
-    // this thread's value row in chunk c (clamped re-reads past the end)
-    auto fetch_row = [&](int c, v4f *r) {
+    const int piece = lane % PPL, krow = lane / PPL;  // this lane's piece and row of a key load
+    const int vpiece = lane & 7, vrow = lane >> 3;    // ... and of a value load (32 dimensions)
+    // (clamped re-reads past the last key: in bounds, never stored)
+    auto fetch_keys = [&](int j0, v4f *kr) {
 #pragma unroll
-        for (int e = 0; e < kWeighDims / 4; e++)
-            r[e] = *reinterpret_cast<const v4f *>(vbase + size_t(min(c * kExactChunk + tid, keys - 1)) * D + 4 * e);
+        for (int e = 0; e < NI; e++)
+            kr[e] = *reinterpret_cast<const v4f *>(kbase + size_t(min(j0 + e * KPI + krow, keys - 1)) * D + 4 * piece);
     };
-    // the value rows of the first two chunks, requested before the scores
-    v4f va[kWeighDims / 4], vb[kWeighDims / 4];
-    fetch_row(0, va);
-    fetch_row(1, vb);
-    if (tid < D4) reinterpret_cast<v4f *>(qs)[tid] = reinterpret_cast<const v4f *>(a.qkv + size_t(head) * D)[tid];
+    auto fetch_rows = [&](int c, v4f *v) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int j = min(c * kExactChunk + wave * 64 + 8 * e + vrow, keys - 1);
+            v[e] = *reinterpret_cast<const v4f *>(vbase + size_t(j) * D + 4 * vpiece);
+        }
+    };
+    const v4f qp = *reinterpret_cast<const v4f *>(a.qkv + size_t(head) * D + 4 * piece);
+    v4f ka[NI], kb[NI];  // two batches of keys, named sets (a dynamically indexed pair spills)
+    fetch_keys(wave * BATCH, ka);
+    if (STEP < keys) fetch_keys(STEP + wave * BATCH, kb);
     const float scale = 1.0f / sqrtf(float(D));
     float local_max = -INFINITY;
-    for (int j0 = 0; j0 < keys; j0 += PASS * kExactChunk) {
-        v4f kr[PASS][D4];
+    // one batch: keys j0 .. j0 + BATCH - 1 of this wave
+    auto batch = [&](int j0, const v4f *kr) {
 #pragma unroll
-        for (int u = 0; u < PASS; u++)
+        for (int e = 0; e < NI; e++) {
+            const int r = e * KPI + krow;
+            const v4f x = kr[e];
+            *reinterpret_cast<v4f *>(stage + r * D + 4 * (piece ^ (r & 15))) = v4f{qp.x * x.x, qp.y * x.y, qp.z * x.z, qp.w * x.w};
+        }
+        // a wave's LDS accesses complete in order: the writes above precede the reads below
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < BATCH) {
+            // the row's pieces in runs of eight, two register sets in turn (reads ahead)
+            const float *row = stage + lane * D;
+            constexpr int RUNS = PPL / 8;
+            v4f A[8], B[8];
+            auto load = [&](v4f *r, int g) {
 #pragma unroll
-            for (int e = 0; e < D4; e++)
-                kr[u][e] = *reinterpret_cast<const v4f *>(kbase + size_t(min(j0 + u * kExactChunk + tid, keys - 1)) * D + 4 * e);
-        __syncthreads();  // the query (first pass)
-#pragma unroll
-        for (int u = 0; u < PASS; u++) {
-            const int j = j0 + u * kExactChunk + tid;
+                for (int u = 0; u < 8; u++) r[u] = *reinterpret_cast<const v4f *>(row + 4 * ((8 * g + u) ^ (lane & 15)));
+            };
             float s = -0.0f;  // dot_f32 in index order (arch/scalar.rs:340-342)
+            auto add = [&](const v4f *r) {
 #pragma unroll
-            for (int e = 0; e < D4; e++) {
-                const v4f qv = reinterpret_cast<const v4f *>(qs)[e];
-                s = s + qv.x * kr[u][e].x;
-                s = s + qv.y * kr[u][e].y;
-                s = s + qv.z * kr[u][e].z;
-                s = s + qv.w * kr[u][e].w;
+                for (int u = 0; u < 8; u++) {
+                    s = s + r[u].x;
+                    s = s + r[u].y;
+                    s = s + r[u].z;
+                    s = s + r[u].w;
+                }
+            };
+            load(A, 0);
+#pragma unroll
+            for (int g = 0; g < RUNS; g += 2) {
+                if (g + 1 < RUNS) load(B, g + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                add(A);
+                if (g + 2 < RUNS) load(A, g + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                if (g + 1 < RUNS) add(B);
             }
-            if (j < keys) {
-                w[j] = s * scale;
+            if (j0 + lane < keys) {
+                w[j0 + lane] = s * scale;
                 local_max = fmaxf(local_max, s * scale);
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    for (int s0 = 0; s0 < keys; s0 += 2 * STEP) {
+        batch(s0 + wave * BATCH, ka);
+        if (s0 + 2 * STEP < keys) fetch_keys(s0 + 2 * STEP + wave * BATCH, ka);
+        if (s0 + STEP < keys) {
+            batch(s0 + STEP + wave * BATCH, kb);
+            if (s0 + 3 * STEP < keys) fetch_keys(s0 + 3 * STEP + wave * BATCH, kb);
+        }
     }
+    // the value rows of the first two chunks, requested only now: held across the scores they
+    // would take registers the keys need, and the softmax hides their latency
+    v4f va[8], vb[8];
+    fetch_rows(0, va);
+    if (kExactChunk < keys) fetch_rows(1, vb);
     const float peak = attn_block_max(local_max, red);  // its barriers publish the scores
     for (int j = tid; j < keys; j += kAttnThreads) w[j] = ref_exp(w[j] - peak);
     __syncthreads();
@@ -381,29 +442,44 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
     const float total = red[8];
     for (int j = tid; j < keys; j += kAttnThreads) w[j] = w[j] / total;
     float o = 0.0f;  // lanes 0..31 of wave 0: output d0 + lane
-    // Chunk c from the registers `v`: its products into LDS, then (lanes 0..31) their ordered
-    // sums, while `v` is refilled with chunk c + 2.
-    auto chunk = [&](int c, v4f *v) {
+    // Chunk c's products from the registers `v` into `buf` (every weight read before the first
+    // product is written: the compiler cannot tell the two regions apart)
+    auto products = [&](int c, const v4f *v, float *buf) {
         const int j0 = c * kExactChunk, n = min(kExactChunk, keys - j0);
-        __syncthreads();  // the weights (first chunk); the previous chunk's products all added
-        {
-            const float wj = tid < n ? w[j0 + tid] : 0.0f;
-            float *col = prod + tid;
+        float wj[8];
 #pragma unroll
-            for (int e = 0; e < kWeighDims / 4; e++) {
-                col[(4 * e) * kProdRow] = wj * v[e].x;
-                col[(4 * e + 1) * kProdRow] = wj * v[e].y;
-                col[(4 * e + 2) * kProdRow] = wj * v[e].z;
-                col[(4 * e + 3) * kProdRow] = wj * v[e].w;
-            }
+        for (int e = 0; e < 8; e++) {
+            const int r = wave * 64 + 8 * e + vrow;
+            wj[e] = r < n ? w[j0 + r] : 0.0f;
         }
-        __syncthreads();
-        if (j0 + 2 * kExactChunk < keys) fetch_row(c + 2, v);
-        if (tid < kWeighDims) o = chain_sum(o, n, prod + tid * kProdRow);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float *col = buf + 4 * vpiece * kProdRow + wave * 64 + 8 * e + vrow;
+            col[0] = wj[e] * v[e].x;
+            col[kProdRow] = wj[e] * v[e].y;
+            col[2 * kProdRow] = wj[e] * v[e].z;
+            col[3 * kProdRow] = wj[e] * v[e].w;
+        }
     };
-    for (int c = 0; c * kExactChunk < keys; c += 2) {
-        chunk(c, va);
-        if ((c + 1) * kExactChunk < keys) chunk(c + 1, vb);
+    // Step k: after the barrier chunk k's products are whole and chunk k - 1's sums are done, so
+    // every wave forms chunk k + 1's products into the other buffer (and requests chunk k + 3 into
+    // the freed registers) while lanes 0..31 of wave 0 add chunk k's.
+    const int chunks = (keys + kExactChunk - 1) / kExactChunk;
+    float *const buf0 = prod, *const buf1 = prod + kWeighDims * kProdRow;
+    auto step = [&](int k, v4f *vnext, float *bnext, const float *bcur) {
+        __syncthreads();
+        if (k + 1 < chunks) {
+            products(k + 1, vnext, bnext);
+            if (k + 3 < chunks) fetch_rows(k + 3, vnext);
+        }
+        if (tid < kWeighDims) o = chain_sum(o, min(kExactChunk, keys - k * kExactChunk), bcur + tid * kProdRow);
+    };
+    __syncthreads();  // the weights
+    products(0, va, buf0);
+    if (2 < chunks) fetch_rows(2, va);
+    for (int k = 0; k < chunks; k += 2) {
+        step(k, vb, buf1, buf0);
+        if (k + 1 < chunks) step(k + 1, va, buf0, buf1);
     }
     // the 32 outputs quantized as one group (eight lanes, four values each)
     __syncthreads();
@@ -755,11 +831,20 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
     const int group = int(sh.heads / sh.kv_heads);
     m->score_smem = size_t(kScoreKeys * (D + 1) + group * D) * 4;
     m->weigh_smem = size_t(kWeighKeys * (kWeighDims + 1) + sh.capacity + 8 * kWeighDims + 16) * 4;
-    m->exact_smem = size_t(D + (sh.capacity + 15) / 16 * 16 + kWeighDims * kProdRow + 16) * 4;
+    m->exact_smem = exact_attention_smem(sh.capacity);
     if (group * D > 4 * kAttnThreads || m->score_smem > 64 * 1024 || m->weigh_smem > 64 * 1024 ||
-        m->exact_smem > 64 * 1024) {
+        m->exact_smem > 160 * 1024) {
         delete m;
         return set_error(FG_ERR_SHAPE, "fg_qwen2_create: the attention does not fit (heads per KV head x head_dim <= 1024, capacity)");
+    }
+    if (sh.exact && (D == 64 || D == 128)) {
+        // the one-launch exact attention takes more LDS than the default limit
+        const void *f = D == 64 ? reinterpret_cast<const void *>(attn_exact_kernel<64>) : reinterpret_cast<const void *>(attn_exact_kernel<128>);
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(m->exact_smem));
+        if (e != hipSuccess) {
+            delete m;
+            return set_error(FG_ERR_HIP, std::string("fg_qwen2_create: ") + hipGetErrorString(e));
+        }
     }
     const size_t widest = std::max(sh.hidden, std::max(width, sh.ffn));
     const size_t padded_vocab = table->quads * 4;

@@ -76,6 +76,19 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int dot4(int a, int b, int acc) { return __builtin_amdgcn_sdot4(a, b, acc, false); }
 
+// A workgroup barrier for pipelines of direct global-to-LDS loads. __syncthreads() carries a
+// release fence, and that fence waits for every outstanding global load of the wave, the direct
+// loads of later stages included, so a pipeline several stages deep would drain to one stage at
+// each barrier. Here each wave first waits for its own loads of the stage it needs (an explicit
+// vmcnt wait before the call); the barrier then publishes them, and the LDS reads of the stage
+// before are complete (lgkmcnt(0)) before any wave refills its buffer.
+__device__ __forceinline__ void stage_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // The partner lane's value in pairs (lane ^ 1), through DPP.
 __device__ __forceinline__ int xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
 // lane ^ 2 within a quad, and the mirror lane within 8 (lane ^ 7), through DPP.

@@ -602,8 +602,16 @@ __global__ __launch_bounds__(256) void gemm16_stream_kernel(GemmParams p)
         }
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // the terms in group order; blocks past the last skipped (a uniform branch, last stage only)
-    auto rescale = [&](const Prods &r, int live) {
+    // the terms in group order; in the last stage blocks past the last are skipped (uniform
+    // branches, kept out of the loop: a branch per block would split the loop body into blocks
+    // the scheduler cannot interleave with the reads and products)
+    auto rescale = [&](const Prods &r) {
+#pragma unroll
+        for (int b = 0; b < KS; b++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] = acc[v] + float(r.d[b][v]) * r.p[b / 4][4 * (b % 4) + v];
+    };
+    auto rescale_last = [&](const Prods &r, int live) {
 #pragma unroll
         for (int b = 0; b < KS; b++) {
             if (b < live) {
@@ -617,20 +625,18 @@ __global__ __launch_bounds__(256) void gemm16_stream_kernel(GemmParams p)
     for (int k = 0; k < DEPTH - 1; k++)
         if (k < stages) issue(k, k);
     Prods prev;
-    int prev_live = 0;
     for (int st = 0; st < stages; st++) {
         // this wave's loads of stage st: the later stages issued so far may still be in flight
         if (st + DEPTH - 2 < stages) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((DEPTH - 2) * T::LOADS) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // every wave's loads of stage st; every wave done reading stage st - 1
+        stage_barrier();  // every wave's loads of stage st; every wave done reading stage st - 1
         if (st + DEPTH - 1 < stages) issue(st + DEPTH - 1, (st + DEPTH - 1) % DEPTH);
         Ops o;
         read(stream_lds + (st % DEPTH) * kStage, o);
-        if (st > 0) rescale(prev, prev_live);  // while the reads are in flight
+        if (st > 0) rescale(prev);  // stage st - 1 (whole), while the reads are in flight
         multiply(o, prev);
-        prev_live = min(KS, B - st * KS);
     }
-    rescale(prev, prev_live);
+    rescale_last(prev, B - (stages - 1) * KS);
     const int n = p.col_begin + tx * 64 + wave * 16 + c;
     if (n >= p.col_end) return;
 #pragma unroll

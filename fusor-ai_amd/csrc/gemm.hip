@@ -461,26 +461,24 @@ __global__ __launch_bounds__(64) void gemm16_kernel(GemmParams p)
     }
 }
 
-// At most 16 rows over many columns, streamed: a workgroup of four waves owns 64 columns (16
-// quads), wave w the 16 x 16 tile of quads 4w .. 4w + 3. The operands of kStreamBlocks blocks (a
-// stage) arrive by direct global-to-LDS loads (lane l of a load writes 16 bytes, or 4, at its base
-// + 16·l, or 4·l), DEPTH - 1 stages ahead of the stage being multiplied, so tens of kilobytes per
-// workgroup are in flight with no register held for them. In every load four neighbouring lanes
-// read one run of bytes (lanes that each touch another line cost the address unit a cycle apiece),
-// and every layout spreads a wave's reads of a block over the banks:
+// The LDS stage of the small-batch products over many columns (at most 16 rows): a workgroup owns
+// 16 rows x 64 columns (16 quads, four 16 x 16 tiles). The operands of kStreamBlocks blocks (a
+// stage) arrive by direct global-to-LDS loads (lane l of a load writes 16 bytes, or 4, at its
+// base + 16·l, or 4·l), so kilobytes per workgroup are in flight with no register held for
+// them. In every load four neighbouring lanes read one run of bytes (lanes that each touch
+// another line cost the address unit a cycle apiece), and every layout spreads a wave's reads of
+// a block over the banks:
 //   W  [16 quads][kStreamBlocks][QB]  the quads' weight bytes, a quad's run of blocks being one run
 //                                     of bytes in the table; a quad every WQ bytes;
-//   WS [4 waves][4 quads][16 slots][4] the weight scales of a quad's blocks, slot k holding block
+//   WS [4 tiles][4 quads][16 slots][4] the weight scales of a quad's blocks, slot k holding block
 //                                     k + 2·quad (mod 16): the four quads' reads of one block fall
 //                                     on different banks;
 //   A  [8 groups][16 rows][4][16 B]   the activation levels, group g holding bytes 64g .. 64g + 63
 //                                     of each row's stage, row r's piece p at position p ^ (r/2 % 4):
 //                                     the 16 rows' pieces of a block fall on eight bank offsets;
 //   AS [4 groups][16 rows][4]         the activation scales, group j holding blocks 4j .. 4j + 3.
-// Each wave waits for its own loads of a stage, then one barrier publishes the stage and frees the
-// buffer the next issue refills. Rows and columns past the edges re-read the last valid one;
-// blocks past the last are loaded clamped (in bounds) and skipped. The arithmetic is
-// gemm16_kernel's.
+// Rows and columns past the edges re-read the last valid one; blocks past the last are loaded
+// clamped (in bounds) and skipped. The arithmetic is gemm16_kernel's.
 constexpr int kStreamBlocks = 16;
 
 template <int FMT>
@@ -492,22 +490,44 @@ struct StreamTile {
     static constexpr int A_BYTES = kStreamBlocks * 32 * 16;
     static constexpr int AS_BYTES = kStreamBlocks * 16 * 4;
     static constexpr int STAGE = W_BYTES + WS_BYTES + A_BYTES + AS_BYTES;
-    static constexpr int DEPTH = FMT == 8 ? 3 : 4;             // stages in LDS
     static constexpr int W_LOADS = kStreamBlocks * QB / 1024;  // per quad
-    static constexpr int LOADS = 4 * W_LOADS + 1 + 2 + 1;      // per wave and stage
-    static constexpr int LDS = DEPTH * STAGE;
-    static_assert(LDS <= 160 * 1024 && (DEPTH - 2) * LOADS < 64, "stream tile");
+};
+
+// At most 16 rows over many columns, two waves per 16 x 16 tile: a workgroup of eight waves owns
+// 64 columns (16 quads) with the LDS stages above, and tile t (quads 4t .. 4t + 3) has two
+// waves. In each stage of kStreamBlocks blocks, wave t forms the products of blocks
+// 0..7 and wave t + 4 those of blocks 8..15; wave t + 4 turns its products into the terms
+// fl(fl(D)·fl(ws·as)) and hands them over through LDS, and after the next barrier wave t adds
+// the stage's sixteen terms per output in group order (its own eight, then the eight handed
+// over). With two waves per SIMD each hides the other's waits (one wave per SIMD leaves every
+// LDS read and product latency exposed). The eight waves share each stage's direct loads
+// evenly: two quads' weight bytes each, the weight scales (first waves) or the activation
+// scales (second waves), and one group of the activation levels. Each wave waits for its own
+// loads of a stage, then one barrier publishes the stage (and the terms handed over the stage
+// before) and frees the buffer the next issue refills.
+template <int FMT>
+struct PairTile {
+    using S = StreamTile<FMT>;
+    static constexpr int HALF = kStreamBlocks / 2;             // blocks per wave and stage
+    static constexpr int DEPTH = 2;                            // stages in LDS (measured: 3 slower)
+    static constexpr int TERMS = 2 * 4 * HALF * 64 * 16;       // [2][4 tiles][HALF][64 lanes] v4f
+    static constexpr int LOADS = 2 * S::W_LOADS + 2;           // per wave and stage
+    static constexpr int LDS = DEPTH * S::STAGE + TERMS;
+    static_assert(LDS <= 160 * 1024 && (DEPTH - 2) * LOADS < 64 && HALF % 4 == 0, "pair tile");
 };
 
 template <int FMT>
-__global__ __launch_bounds__(256) void gemm16_stream_kernel(GemmParams p)
+__global__ __launch_bounds__(512) void gemm16_pair_kernel(GemmParams p)
 {
-    using T = StreamTile<FMT>;
-    constexpr int QB = T::QB, WQ = T::WQ, DEPTH = T::DEPTH, KS = kStreamBlocks, kWLoads = T::W_LOADS;
-    constexpr int kStage = T::STAGE, kW = T::W_BYTES, kWS = T::WS_BYTES, kA = T::A_BYTES;
-    extern __shared__ __align__(16) unsigned char stream_lds[];  // [DEPTH][STAGE]
+    using S = StreamTile<FMT>;
+    using T = PairTile<FMT>;
+    constexpr int QB = S::QB, WQ = S::WQ, DEPTH = T::DEPTH, KS = kStreamBlocks, HALF = T::HALF, kWLoads = S::W_LOADS;
+    constexpr int kStage = S::STAGE, kW = S::W_BYTES, kWS = S::WS_BYTES, kA = S::A_BYTES;
+    extern __shared__ __align__(16) unsigned char pair_lds[];  // [DEPTH][STAGE], then the handed terms
+    v4f *const handed = reinterpret_cast<v4f *>(pair_lds + DEPTH * kStage);
     const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, s = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = wave & 3, h = wave >> 2;  // h 0: blocks 0..7 and the sums; h 1: blocks 8..15
     int tx, ty;
     tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 63) / 64, (p.M + 15) / 16, tx, ty);
     const int m0 = ty * 16, q0 = (p.col_begin >> 2) + tx * 16, last_quad = (p.col_end - 1) >> 2;
@@ -515,109 +535,121 @@ __global__ __launch_bounds__(256) void gemm16_stream_kernel(GemmParams p)
     const int stages = (B + KS - 1) / KS;
 
     auto issue = [&](int st, int buf) {
-        unsigned char *base = stream_lds + buf * kStage;
+        unsigned char *base = pair_lds + buf * kStage;
         const int b0 = st * KS;
-        // this wave's four quads' weight bytes (clamped to the quad's last 16 bytes)
+        // the weight bytes of quads 4·tile + 2h and 4·tile + 2h + 1
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            const int8_t *qbase = p.codes + size_t(min(q0 + 4 * wave + qq, last_quad)) * B * QB;
+        for (int qq = 0; qq < 2; qq++) {
+            const int ql = 4 * tile + 2 * h + qq;
+            const int8_t *qbase = p.codes + size_t(min(q0 + ql, last_quad)) * B * QB;
 #pragma unroll
             for (int j = 0; j < kWLoads; j++) {
                 const int at = min(b0 * QB + (j * 64 + lane) * 16, B * QB - 16);
-                __builtin_amdgcn_global_load_lds(qbase + at, base + (4 * wave + qq) * WQ + j * 1024, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(qbase + at, base + ql * WQ + j * 1024, 16, 0, 0);
             }
         }
-        {
-            // weight scales: lane l, quad 4·wave + l / 16, slot l % 16 (block slot + 2·quad mod 16)
+        if (h == 0) {
+            // the tile's weight scales: lane l, quad 4·tile + l / 16, slot l % 16 (block slot +
+            // 2·quad mod 16)
             const int qw = lane >> 4, slot = lane & 15;
-            const int q = min(q0 + 4 * wave + qw, last_quad), blk = min(b0 + ((slot + 2 * qw) & 15), B - 1);
-            __builtin_amdgcn_global_load_lds(p.wscales + (size_t(q) * G + blk) * 4, base + kW + wave * 1024, 16, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            // activation group g = 2·wave + j: lane l, row r = l / 4, position l % 4 holding piece
-            // (l % 4) ^ (r / 2 % 4)
-            const int g = 2 * wave + j, r = lane >> 2, piece = (lane & 3) ^ ((r >> 1) & 3);
-            const int row = min(m0 + r, p.M - 1), at = min(b0 * 32 + (4 * g + piece) * 16, K - 16);
-            __builtin_amdgcn_global_load_lds(p.q + size_t(row) * K + at, base + kW + kWS + g * 1024, 16, 0, 0);
+            const int q = min(q0 + 4 * tile + qw, last_quad), blk = min(b0 + ((slot + 2 * qw) & 15), B - 1);
+            __builtin_amdgcn_global_load_lds(p.wscales + (size_t(q) * G + blk) * 4, base + kW + tile * 1024, 16, 0, 0);
+        } else {
+            // activation scales of group `tile`: lane l, row l / 4, block 4·tile + l % 4
+            const int row = min(m0 + (lane >> 2), p.M - 1), blk = min(b0 + 4 * tile + (lane & 3), B - 1);
+            __builtin_amdgcn_global_load_lds(p.as + size_t(row) * G + blk, base + kW + kWS + kA + tile * 256, 4, 0, 0);
         }
         {
-            // activation scales of group `wave`: lane l, row l / 4, block 4·wave + l % 4
-            const int row = min(m0 + (lane >> 2), p.M - 1), blk = min(b0 + 4 * wave + (lane & 3), B - 1);
-            __builtin_amdgcn_global_load_lds(p.as + size_t(row) * G + blk, base + kW + kWS + kA + wave * 256, 4, 0, 0);
+            // activation group g = wave: lane l, row r = l / 4, position l % 4 holding piece
+            // (l % 4) ^ (r / 2 % 4)
+            const int r = lane >> 2, piece = (lane & 3) ^ ((r >> 1) & 3);
+            const int row = min(m0 + r, p.M - 1), at = min(b0 * 32 + (4 * wave + piece) * 16, K - 16);
+            __builtin_amdgcn_global_load_lds(p.q + size_t(row) * K + at, base + kW + kWS + wave * 1024, 16, 0, 0);
         }
     };
 
     const int shift = FMT == 8 ? 0 : 4 * (s >> 1);
-    const int w_off = (4 * wave + (c >> 2)) * WQ + (c & 3) * (QB / 4) + (FMT == 8 ? 8 * s : 8 * (s & 1));
-    // block b of row c: group b / 2, piece 2·(b % 2) + s / 2 at position piece ^ (c / 2 % 4)
+    const int w_off = (4 * tile + (c >> 2)) * WQ + (c & 3) * (QB / 4) + (FMT == 8 ? 8 * s : 8 * (s & 1));
     const int a_row = kW + kWS + c * 64 + 8 * (s & 1), sig = (c >> 1) & 3;
     const int a_off0 = a_row + ((s >> 1) ^ sig) * 16, a_off1 = a_row + ((2 + (s >> 1)) ^ sig) * 16;
-    // the scale products' operands: lane l gives block 4j + l / 16's scale of row (or column)
-    // l % 16; the weight scale of column i, block k sits in quad i / 4's slot k - 2·(i / 4)
     const int blk4 = lane >> 4, qi = c >> 2;
     const int as_off = kW + kWS + kA + (c * 4 + blk4) * 4;
-    const int ws_row = kW + wave * 1024 + qi * 256 + (c & 3) * 4;
-
-    // One stage's operands in registers: with one wave per SIMD nothing hides a read's latency but
-    // the wave's own other work, so a stage's reads go out before the previous stage's rescale.
+    const int ws_row = kW + tile * 1024 + qi * 256 + (c & 3) * 4;
     struct Ops {
-        long w[KS], a[KS];
-        float as[KS / 4], ws[KS / 4];
+        long w[HALF], a[HALF];
+        float as[HALF / 4], ws[HALF / 4];
     };
-    // The products of a stage: the int8 group sums, and the scale products fl(ws·as) of four
-    // blocks at a time from one f32 MFMA outer product (v_mfma_f32_16x16x1_4b: block k of the four
-    // in results 4k .. 4k + 3, the layout of the int8 sums; exactly the VALU's rounded products).
     struct Prods {
-        v4i d[KS];
-        v16f p[KS / 4];
+        v4i d[HALF];
+        v16f p[HALF / 4];
     };
+    // this wave's blocks HALF·h + j of the stage in `base`
     auto read = [&](const unsigned char *base, Ops &o) {
 #pragma unroll
-        for (int b = 0; b < KS; b++) {
-            o.w[b] = *reinterpret_cast<const long *>(base + w_off + b * QB);
-            o.a[b] = *reinterpret_cast<const long *>(base + (b & 1 ? a_off1 : a_off0) + (b >> 1) * 1024);
+        for (int j = 0; j < HALF; j++) {
+            const int b = HALF * h + j;
+            o.w[j] = *reinterpret_cast<const long *>(base + w_off + b * QB);
+            o.a[j] = *reinterpret_cast<const long *>(base + (j & 1 ? a_off1 : a_off0) + (b >> 1) * 1024);
         }
 #pragma unroll
-        for (int j = 0; j < KS / 4; j++) {
-            o.as[j] = *reinterpret_cast<const float *>(base + as_off + j * 256);
-            o.ws[j] = *reinterpret_cast<const float *>(base + ws_row + ((4 * j + blk4 - 2 * qi) & 15) * 16);
+        for (int j = 0; j < HALF / 4; j++) {
+            const int J = HALF / 4 * h + j;  // group of four blocks
+            o.as[j] = *reinterpret_cast<const float *>(base + as_off + J * 256);
+            o.ws[j] = *reinterpret_cast<const float *>(base + ws_row + ((4 * J + blk4 - 2 * qi) & 15) * 16);
         }
     };
     auto multiply = [&](const Ops &o, Prods &r) {
 #pragma unroll
-        for (int j = 0; j < KS / 4; j++) {
+        for (int j = 0; j < HALF / 4; j++) {
             const v16f zero16 = {0};
             r.p[j] = __builtin_amdgcn_mfma_f32_16x16x1f32(o.as[j], o.ws[j], zero16, 0, 0, 0);
         }
 #pragma unroll
-        for (int b = 0; b < KS; b++) {
-            long x = o.w[b];
+        for (int j = 0; j < HALF; j++) {
+            long x = o.w[j];
             if (FMT == 4) {
                 const int lo = nibbles_signed(int(x) >> shift), hi = nibbles_signed(int(x >> 32) >> shift);
                 x = long(unsigned(lo)) | (long(hi) << 32);
             }
             const v4i zero = {0, 0, 0, 0};
-            r.d[b] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[b], x, zero, 0, 0, 0);
+            r.d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a[j], x, zero, 0, 0, 0);
         }
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // the terms in group order; in the last stage blocks past the last are skipped (uniform
-    // branches, kept out of the loop: a branch per block would split the loop body into blocks
-    // the scheduler cannot interleave with the reads and products)
-    auto rescale = [&](const Prods &r) {
+    // the first wave's own terms of a stage, then the handed-over ones, in group order; in the
+    // last stage blocks past the last are skipped (uniform branches, kept out of the loop)
+    auto own = [&](const Prods &r, int live) {
 #pragma unroll
-        for (int b = 0; b < KS; b++)
+        for (int j = 0; j < HALF; j++) {
+            if (j < live) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) acc[v] = acc[v] + float(r.d[b][v]) * r.p[b / 4][4 * (b % 4) + v];
-    };
-    auto rescale_last = [&](const Prods &r, int live) {
-#pragma unroll
-        for (int b = 0; b < KS; b++) {
-            if (b < live) {
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] = acc[v] + float(r.d[b][v]) * r.p[b / 4][4 * (b % 4) + v];
+                for (int v = 0; v < 4; v++) acc[v] = acc[v] + float(r.d[j][v]) * r.p[j / 4][4 * (j % 4) + v];
             }
+        }
+    };
+    auto theirs = [&](int buf, int live) {
+        const v4f *t = handed + (buf * 4 + tile) * HALF * 64 + lane;
+        v4f x[HALF];
+#pragma unroll
+        for (int j = 0; j < HALF; j++) x[j] = t[j * 64];
+#pragma unroll
+        for (int j = 0; j < HALF; j++) {
+            if (j < live) {
+                acc[0] = acc[0] + x[j].x;
+                acc[1] = acc[1] + x[j].y;
+                acc[2] = acc[2] + x[j].z;
+                acc[3] = acc[3] + x[j].w;
+            }
+        }
+    };
+    auto hand_over = [&](const Prods &r, int buf) {
+        v4f *t = handed + (buf * 4 + tile) * HALF * 64 + lane;
+#pragma unroll
+        for (int j = 0; j < HALF; j++) {
+            v4f x;
+#pragma unroll
+            for (int v = 0; v < 4; v++) x[v] = float(r.d[j][v]) * r.p[j / 4][4 * (j % 4) + v];
+            t[j * 64] = x;
         }
     };
 
@@ -629,24 +661,39 @@ __global__ __launch_bounds__(256) void gemm16_stream_kernel(GemmParams p)
         // this wave's loads of stage st: the later stages issued so far may still be in flight
         if (st + DEPTH - 2 < stages) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((DEPTH - 2) * T::LOADS) : "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        stage_barrier();  // every wave's loads of stage st; every wave done reading stage st - 1
+        // every wave's loads of stage st and the terms of stage st - 1 handed over; every wave done
+        // reading stage st - 1 and the terms of stage st - 2
+        stage_barrier();
         if (st + DEPTH - 1 < stages) issue(st + DEPTH - 1, (st + DEPTH - 1) % DEPTH);
         Ops o;
-        read(stream_lds + (st % DEPTH) * kStage, o);
-        if (st > 0) rescale(prev);  // stage st - 1 (whole), while the reads are in flight
-        multiply(o, prev);
+        read(pair_lds + (st % DEPTH) * kStage, o);
+        if (h == 0) {
+            if (st > 0) {
+                own(prev, HALF);  // stage st - 1 (whole), while the reads are in flight
+                theirs((st - 1) & 1, HALF);
+            }
+            multiply(o, prev);
+        } else {
+            Prods mine;
+            multiply(o, mine);
+            hand_over(mine, st & 1);
+        }
     }
-    rescale_last(prev, B - (stages - 1) * KS);
-    const int n = p.col_begin + tx * 64 + wave * 16 + c;
+    stage_barrier();  // the last stage's handed-over terms
+    if (h != 0) return;
+    const int live = B - (stages - 1) * KS;
+    own(prev, live);
+    theirs((stages - 1) & 1, live - HALF);
+    const int n = p.col_begin + tx * 64 + tile * 16 + c;
     if (n >= p.col_end) return;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
         const int r = m0 + 4 * s + v;
         if (r >= p.M) continue;
-        float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+        float *out = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
         float y = acc[v];
         if (p.bias && n < p.n_rows) y = y + p.bias[n];
-        *o = p.accumulate ? *o + y : y;
+        *out = p.accumulate ? *out + y : y;
     }
 }
 
@@ -942,10 +989,10 @@ int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
         // more tiles: four adjacent column tiles per workgroup, their operands streamed through LDS
         if (!dots && !FUSED) {
             const dim3 sgrid(unsigned(((ncols + 63) / 64) * ((p.M + 15) / 16)));
-            constexpr int lds = StreamTile<FMT>::LDS;
-            FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm16_stream_kernel<FMT>),
+            constexpr int lds = PairTile<FMT>::LDS;
+            FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm16_pair_kernel<FMT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-            gemm16_stream_kernel<FMT><<<sgrid, 256, size_t(lds), s>>>(p);
+            gemm16_pair_kernel<FMT><<<sgrid, 512, size_t(lds), s>>>(p);
             FG_HIP(hipGetLastError());
             return FG_OK;
         }

@@ -394,10 +394,12 @@ def test_int4_shape_bit_exact(fk, rows):
 
 
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
-@pytest.mark.parametrize("rows,k", [(5, 32 * 8), (16, 32 * 8), (9, 32 * 17)])
+@pytest.mark.parametrize("rows,k", [(5, 32 * 8), (16, 32 * 8), (9, 32 * 17), (12, 32 * 28), (7, 32 * 3)])
 def test_small_batch_streamed_with_one_or_two_stages(fk, dtype, rows, k):
-    """The streamed small-batch product with fewer blocks than one stage of 16 (8 blocks), and one
-    whole stage and a single block of a second (17 blocks); 5-16 rows, 8228 columns."""
+    """The streamed small-batch product with fewer blocks than one stage of 16 (8 or 3 blocks),
+    and one whole stage and 1 or 12 blocks of a second (17, 28 blocks: a tile's two waves split
+    each stage's blocks 8 and 8, so the last stage's terms come from the first wave alone or from
+    both); 5-16 rows, 8228 columns."""
     n = 8228
     data = synthetic_table(dtype, n, k, seed=rows + k)
     t = table(fk, dtype, n, k, data)

@@ -787,7 +787,9 @@ __global__ __launch_bounds__(256) void gemm16_split_kernel(GemmParams p)
 // for kStageBlocks blocks at a time (a stage) are staged in LDS once and read by every wave:
 //   A  [kb][BM rows][32 B]   int8 activation levels (q, row-major [M][K]);
 //   W  [kb][BN cols][32 B]   weight levels (Q8; Q4: [kb][BN cols][16 B] packed nibbles);
-//   AS [kb][BM]              activation scales, from the block-major copy as_t [G][Mpad];
+//   AS [kb][BM]              activation scales, from the block-major copy as_t [G][Mpad] (f32
+//                            rows are quantized straight into it), or from the pre-quantized
+//                            rows' own [M][G] scales by 4-byte loads;
 //   WS [kb][BN/4 quads][4]   weight scales, the table's own order ((q·G + g)·4 + lane).
 // Every stage arrives by direct global-to-LDS loads (global_load_lds_dwordx4: lane l writes 16 bytes
 // at base + 16·l), so no register holds staged data and the loads take no VALU work. Two stage
@@ -830,6 +832,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p)
     // drops the kernel's host-side launch stub.)
     unsigned char *const w_lds = stage_lds + T::A_BYTES, *const as_lds = w_lds + T::W_BYTES, *const ws_lds = as_lds + T::AS_BYTES;
     constexpr int kStage = T::STAGE, kALoads = T::A_LOADS, kWLoads = T::W_LOADS, kASLanes = T::AS_LANES, kWSLanes = T::WS_LANES;
+    constexpr int kASLoads4 = KB * BM / 64;  // 4-byte loads of the row-major scales per stage
     auto issue = [&](int s, int buf) {
         unsigned char *base = stage_lds + buf * kStage;
         const int boff = buf * kStage;
@@ -856,10 +859,20 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p)
             }
             __builtin_amdgcn_global_load_lds(src, w_lds + boff + k * 1024, 16, 0, 0);
         }
-        if (wave == 2 && lane < kASLanes) {
-            // four rows' scales of one block per lane: as_t [G][Mpad], Mpad a multiple of BM
-            const int kb = lane / (BM / 4), r = (lane - kb * (BM / 4)) * 4, blk = min(g0 + kb, B - 1);
-            __builtin_amdgcn_global_load_lds(p.as_t + size_t(blk) * p.Mpad + m0 + r, as_lds + boff, 16, 0, 0);
+        if (p.as_t) {
+            if (wave == 2 && lane < kASLanes) {
+                // four rows' scales of one block per lane: as_t [G][Mpad], Mpad a multiple of BM
+                const int kb = lane / (BM / 4), r = (lane - kb * (BM / 4)) * 4, blk = min(g0 + kb, B - 1);
+                __builtin_amdgcn_global_load_lds(p.as_t + size_t(blk) * p.Mpad + m0 + r, as_lds + boff, 16, 0, 0);
+            }
+        } else {
+            // the rows' own scales as [M][G]: one scale per lane (4-byte loads), lane l of load j
+            // holding position 64j + l of the stage's [KB][BM] (block pos / BM, row pos % BM)
+            for (int j = wave; j < kASLoads4; j += 4) {
+                const int pos = 64 * j + lane, kb = pos / BM, r = pos - kb * BM;
+                const int row = min(m0 + r, p.M - 1), blk = min(g0 + kb, B - 1);
+                __builtin_amdgcn_global_load_lds(p.as + size_t(row) * G + blk, as_lds + boff + j * 256, 4, 0, 0);
+            }
         }
         if (wave == 3 && lane < kWSLanes) {
             // the four lanes' scales of one quad and block per lane
@@ -1179,9 +1192,10 @@ ScratchPlan plan_scratch(const ProductArgs &a)
     }
     pl.tiles = choose_tiles(a);
     if (pl.tiles) {
-        // the staged kernel reads whole tiles of as_t: rows padded to 128
+        // the staged kernel reads whole tiles of as_t (rows padded to 128), which f32 rows are
+        // quantized straight into; pre-quantized rows' own [M][G] scales it reads as they are
         pl.Mpad = int((M + 127) / 128 * 128);
-        pl.t_bytes = G * size_t(pl.Mpad) * 4;
+        pl.t_bytes = a.x ? G * size_t(pl.Mpad) * 4 : 0;
         return pl;
     }
     // The activation scales go to LDS per tile when a tile's fit in 64 KiB and their rows are
@@ -1283,7 +1297,7 @@ int launch_gemm(const ProductArgs &a, hipStream_t s)
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) rc = check_hip(e, "transpose_scales_kernel");
     }
-    const float *as_block = caller_t && t_bytes ? a.as_t : as_t;
+    const float *as_block = caller_t ? a.as_t : (t_bytes ? as_t : nullptr);
     if (rc == FG_OK) {
         GemmParams p{};
         p.codes = t->codes;

@@ -5,6 +5,13 @@
  *
  * Built with -O3 -ffp-contract=off -fno-fast-math: Rust never contracts a + b*c, so neither may
  * this file.
+ *
+ * What pins it (tests/test_oracle.py, tests/test_oracle_attention.py): the reference tests' known
+ * answers and f64 tolerance for the product, closed forms and brute force for the formats and
+ * quantizers, and absorption cases for the order of every f32 sum in the decode glue (RMSNorm,
+ * softmax, weighted values, the exponentials' offset sums). Parity unpinned: the bits of the exp
+ * and exp_fast polynomials, SiLU and the rotary angles, which are checked only against their
+ * stated error bounds.
  */
 #include "fusor_oracle.h"
 
@@ -588,6 +595,20 @@ void or_softmax(float *scores, size_t n)
     for (size_t i = 0; i < n; i++) scores[i] = scores[i] / total;
 }
 
+/* ops::weigh (ops.rs:329-342) on the scalar backend: `scores` replaced by their softmax, then
+ * out = the sum from +0 of w_j·value_j, one key at a time in key order (the default
+ * axpy_f32_many, arch/mod.rs:141-147, over blocks of DOTS keys, then the rest one by one: the
+ * same order); value j at values + j·stride. */
+void or_weigh(float *scores, size_t n, const float *values, size_t stride, size_t dim, float *out)
+{
+    or_softmax(scores, n);
+    for (size_t i = 0; i < dim; i++) out[i] = 0.0f;
+    for (size_t j = 0; j < n; j++) {
+        const float *v = values + j * stride;
+        for (size_t i = 0; i < dim; i++) out[i] = out[i] + scores[j] * v[i];
+    }
+}
+
 /* ------------------------------------------------- int8 attention (blocks/src/attention.rs) */
 
 static size_t pad32(size_t n) { return (n + 31) / 32 * 32; }
@@ -779,13 +800,8 @@ int or_qwen2_layer_forward(const or_qwen2_shape *sh, const or_qwen2_layer *ly, s
         const float *query = qkv + h * D;
         for (size_t j = 0; j <= position; j++)
             scores[j] = or_dot_f32(query, kcache + cache_offset(sh, li, kv, j), D) * scale;
-        or_softmax(scores, position + 1);
-        float *out = attn + h * D;
-        for (size_t i = 0; i < D; i++) out[i] = 0.0f;
-        for (size_t j = 0; j <= position; j++) {
-            const float *v = vcache + cache_offset(sh, li, kv, j);
-            for (size_t i = 0; i < D; i++) out[i] = out[i] + scores[j] * v[i];
-        }
+        /* keys 0..position are whole rows from the head's first (position < capacity) */
+        or_weigh(scores, position + 1, vcache + cache_offset(sh, li, kv, 0), D, D, attn + h * D);
     }
     /* attended_residual: hidden += o(attention) (layer.rs:239-245, linear.rs:134-143) */
     project_row(sh, ly->o, H, width, attn, NULL, y, threads);

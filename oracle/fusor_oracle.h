@@ -129,6 +129,8 @@ void or_rope_angles(const float *inv_freq, size_t half, size_t position, float *
                     float *sin_out);                                     /* rotary.rs angles */
 void or_rope_half(float *head, size_t dim, const float *cos_v, const float *sin_v);
 void or_softmax(float *scores, size_t n);                                /* ops.rs:301-306 */
+void or_weigh(float *scores, size_t n, const float *values, size_t stride, size_t dim,
+              float *out);                                                 /* ops.rs:329-342 */
 
 /* Seeded generator (rng.rs:10-52): SplitMix64-seeded xoshiro256**, Box-Muller normals. */
 typedef struct {

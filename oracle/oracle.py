@@ -85,6 +85,7 @@ def _declare(l):
         "or_rope_angles": (None, [_P, _S, _S, _P, _P]),
         "or_rope_half": (None, [_P, _S, _P, _P]),
         "or_softmax": (None, [_P, _S]),
+        "or_weigh": (None, [_P, _S, _P, _S, _S, _P]),
         "or_rng_new": (None, [_P, ctypes.c_uint64]),
         "or_rng_next_u64": (ctypes.c_uint64, [_P]),
         "or_rng_uniform": (ctypes.c_double, [_P]),
@@ -275,6 +276,16 @@ def softmax(x):
     x = np.array(x, dtype=np.float32)
     lib().or_softmax(_ptr(x), x.size)
     return x
+
+
+def weigh(scores, values):
+    """ops::weigh (ops.rs:329-342): the softmax of `scores` (returned) and the sum of the value
+    rows [n, dim] weighted by it, in key order."""
+    w = np.array(scores, dtype=np.float32)
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.zeros(v.shape[1], np.float32)
+    lib().or_weigh(_ptr(w), w.size, _ptr(v), v.shape[1], v.shape[1], _ptr(out))
+    return w, out
 
 
 class Rng:

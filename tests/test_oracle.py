@@ -361,6 +361,109 @@ def test_rms_norm_and_softmax_against_closed_forms():
     assert abs(float(sm.astype(np.float64).sum()) - 1.0) < 1e-5
 
 
+def _fold(values, start=0.0):
+    """A left fold in f32 (numpy's float32 additions are IEEE single, one rounding each)."""
+    acc = np.float32(start)
+    for v in values:
+        acc = np.float32(acc + np.float32(v))
+    return acc
+
+
+def test_rms_norm_sums_its_squares_from_the_first_in_index_order():
+    """ops.rs:7-16 with dot_f32 (arch/scalar.rs:112-114): the squares added from index 0. One
+    square of 2^24 first absorbs every later square of 1 (2^24 + 1 is a tie that rounds to even,
+    back to 2^24), so the mean is exactly 4096, the inverse exactly 1/64 and the outputs x / 64;
+    summed pairwise, reversed or in blocks the 4095 ones survive (mean 4097) and no output does."""
+    n = 4096
+    x = np.ones(n, np.float32)
+    x[0] = 4096.0
+    got = O.rms_norm(x, np.ones(n, np.float32), 0.0)
+    want = np.full(n, 1.0 / 64.0, np.float32)
+    want[0] = 64.0
+    assert np.array_equal(got, want)
+    assert _fold(x[::-1] * x[::-1]) != np.float32(2.0 ** 24)  # a reversed sum keeps the ones
+
+
+def test_rms_norm_scales_the_normalized_value_by_the_weight_last():
+    """ops.rs:12: output = (value · inverse) · scale. For these one-value rows (mean = v², eps 0,
+    inverse = fl(1/v)) the other association, value · (inverse · scale), rounds differently."""
+    cases = 0
+    for v in range(3, 40):
+        inv = np.float32(np.float32(1.0) / np.float32(np.sqrt(np.float32(v * v))))
+        for w in range(3, 40):
+            left = np.float32(np.float32(np.float32(v) * inv) * np.float32(w))
+            right = np.float32(np.float32(v) * np.float32(inv * np.float32(w)))
+            if left == right:
+                continue
+            got = O.rms_norm(np.array([v], np.float32), np.array([w], np.float32), 0.0)
+            assert got[0] == left and got[0] != right, (v, w)
+            cases += 1
+    assert cases > 20
+
+
+def test_softmax_totals_every_exponential_in_index_order():
+    """ops.rs:302-307: the total is a plain fold over the exponentials (not the sweep's offset
+    sums). Score 0 first (exponential exactly 1), then 511 scores of -18, each exponential under
+    half an ulp of 1: a fold from index 0 absorbs them all, so the total is exactly 1, the first
+    weight exactly 1 and every other weight its exponential unchanged; the eight offset sums of
+    Exponentials::apply, a pairwise sum or a reversed one each total about 1 + 7e-6."""
+    s = np.full(512, -18.0, np.float32)
+    s[0] = 0.0
+    w = O.softmax(s)
+    tiny = O.exp(np.float32(-18.0))
+    assert float(tiny) * 2 < 2.0 ** -24  # under half an ulp of 1
+    assert w[0] == np.float32(1.0)
+    assert np.all(w[1:] == tiny)
+    assert _fold(np.exp(s.astype(np.float32))[::-1]) > np.float32(1.0)  # reversed: not absorbed
+
+
+def test_weighted_values_add_one_key_at_a_time_in_key_order():
+    """ops::weigh (ops.rs:329-342) with the scalar axpy_f32_many (arch/mod.rs:141-147): each
+    output adds w_j·v_j from +0 one key at a time. The weights of the scores above (1, then 511
+    under half an ulp of 1) on rows of ones: in key order the first term is 1 and absorbs every
+    later one, so each output is exactly 1; the terms of a block of DOTS keys summed first, or
+    the keys taken last to first, carry them (about 1 + 7e-6). A dropped first key gives about
+    8e-6, a key's weight applied to the next key's row leaves the row's own bits wrong."""
+    n, dim = 512, 6
+    s = np.full(n, -18.0, np.float32)
+    s[0] = 0.0
+    values = np.ones((n, dim), np.float32)
+    w, out = O.weigh(s, values)
+    assert w[0] == np.float32(1.0) and np.array_equal(w[1:], np.full(n - 1, O.exp(np.float32(-18.0))))
+    assert np.array_equal(out, np.ones(dim, np.float32))
+    blocked = _fold([_fold(w[b:b + 4]) for b in range(0, n, 4)])
+    assert blocked > np.float32(1.0) and _fold(w[::-1]) > np.float32(1.0)
+    # distinct rows: output i is the key-order fold of w_j·v_j[i]
+    rng = np.random.default_rng(8)
+    s = (rng.standard_normal(37) * 3).astype(np.float32)
+    values = rng.standard_normal((37, dim)).astype(np.float32)
+    w, out = O.weigh(s, values)
+    for i in range(dim):
+        assert out[i] == _fold([np.float32(w[j] * values[j, i]) for j in range(37)])
+
+
+@pytest.mark.parametrize("fast", [False, True])
+@pytest.mark.parametrize("tail", [0, 3])
+def test_exponentials_sum_the_tail_then_the_eight_offset_sums(fast, tail):
+    """Exponentials::apply (ops.rs:168-174) with the scalar sweep (arch/scalar.rs:117-125): sums
+    per offset in a run of EXP_RUN = 8 over the whole runs (each from +0 in run order), then a
+    fold from -0 of the values past the last whole run followed by the eight sums. With the one
+    exponential of 1 at offset 0 and the others under half an ulp of 1, offset 0's sum stays 1
+    while offsets 1..7 keep their 64 small terms, so the total exceeds 1 by their seven sums; a
+    plain fold from index 0 would absorb every small term and total exactly 1."""
+    n = 8 * 64 + tail
+    s = np.full(n, -18.0, np.float32)
+    s[0] = 0.0
+    v, total = O.exponentials_apply(s, fast)
+    t = v[1]
+    assert np.all(v[1:] == t) and v[0] == np.float32(1.0)
+    sums = [_fold(v[k:8 * 64:8]) for k in range(8)]
+    assert sums[0] == np.float32(1.0) and sums[1] == _fold([t] * 64)
+    want = _fold(list(v[8 * 64:]) + sums, start=-0.0)
+    assert total == want
+    assert total > np.float32(1.0) and _fold(v) == np.float32(1.0)
+
+
 def test_rotary_angles_against_f64():
     """rotary.rs tests' 1e-6 bound; frequencies base^(-2i/d)."""
     cos, sin = O.rope_tables(1e6, 64, 600)

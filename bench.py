@@ -33,6 +33,8 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "fusor-ai_amd")]
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+# f32 VALU issue without packed instructions: 256 CUs x 4 SIMDs x 16 lanes per cycle x 2.4 GHz
+VALU_LANE_OPS = 256 * 4 * 16 * 2.4e9
 METRIC = "int8 qmatvec weight GB/s (% HBM peak); Qwen2-0.5B-shape decode tokens/sec"
 
 Q7B32, Q4B32, Q8B32 = 1, 2, 4
@@ -361,6 +363,22 @@ def timed(call, iters):
     return time.perf_counter() - t0
 
 
+def gemm_bound(rows, k, n, ms):
+    """The attainable time of an exact-order batched product: the largest of its int8 MFMA time,
+    its HBM time (Q8b32 codes and scales, int8 rows with scales and corrections, f32 outputs) and
+    its VALU time for the per-block rescale (convert, multiply, add per output and 32-deep block,
+    the scale products coming from f32 outer products on the matrix cores)."""
+    groups = k // 32
+    t_mfma = 2.0 * rows * n * k / (INT8_PEAK_TOPS * 1e12)
+    t_hbm = (n * k + n * groups * 4 + rows * k + rows * groups * 8 + rows * n * 4) / (HBM_PEAK_GBS * 1e9)
+    t_valu = 3.0 * rows * n * groups / VALU_LANE_OPS
+    attainable = max(t_mfma, t_hbm, t_valu)
+    return {"t_mfma_us": round(t_mfma * 1e6, 2), "t_hbm_us": round(t_hbm * 1e6, 2),
+            "t_valu_rescale_us": round(t_valu * 1e6, 2),
+            "by": ("valu_rescale" if attainable == t_valu else "hbm" if attainable == t_hbm else "mfma"),
+            "frac_attainable": round(attainable * 1e3 / ms, 4)}
+
+
 def noalloc_product(fk, table, inp, rows, n, out):
     """fg_matmul_noalloc (its scratch a fixed per-device array) over an fk.Input."""
     import ctypes
@@ -453,6 +471,7 @@ def extras(fk, torch, np, with_cpu=True):
                  "TOPS_from": "fg_matmul" if ms_q <= ms_q_na else "fg_matmul_noalloc",
                  "fused_scale_us": round(ms_fused * 1e3, 2), "fused_scale_TOPS": round(ops / ms_fused / 1e9, 1),
                  "fused_scale_frac_int8_peak": round(ops / ms_fused / 1e9 / INT8_PEAK_TOPS, 4)}
+        entry["bound"] = gemm_bound(rows, k, n, ms_best)
         if with_cpu:
             cpu_ops = 2.0 * cpu_rows * n * k
             entry["cpu_baseline"] = cpu_product_baseline(

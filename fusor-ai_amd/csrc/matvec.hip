@@ -54,7 +54,29 @@ int batch_depth(const ProjParams &p, int dtype, int out)
     return mine <= 1 ? 1 : mine <= 2 ? 2 : mine <= 4 ? 4 : 8;
 }
 
+// RMSNorm + quantize of one row (the IN_NORM prologue's arithmetic, exact or parallel order) into
+// q_out, s_out and c_out: the head's input, formed once instead of in each of its workgroups.
+template <bool EXACT>
+__global__ __launch_bounds__(kThreads) void norm_quantize_kernel(ProjParams p)
+{
+    __shared__ __align__(16) float nbuf[4 * 4 * kThreads];
+    __shared__ float red[16];
+    StageRegs g;
+    stage_issue<8, 1, IN_NORM>(p, g);
+    stage_finish<8, 1, IN_NORM, EXACT>(p, g, p.q_out, p.s_out, p.c_out, nbuf, red);
+}
+
 }  // namespace
+
+int launch_norm_quantize(const ProjParams &p, bool exact, hipStream_t s)
+{
+    if (p.K % 32 || p.K > 4 * 4 * kThreads || p.G * 32 != p.K)
+        return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
+    if (exact) norm_quantize_kernel<true><<<1, kThreads, 0, s>>>(p);
+    else norm_quantize_kernel<false><<<1, kThreads, 0, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
 
 size_t proj_smem(const ProjParams &p, int rows, int in, int out)
 {
@@ -94,8 +116,8 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     const size_t smem = proj_smem(p, 1, in, out);
     if (smem > 160 * 1024) return set_error(FG_ERR_SHAPE, "rows too wide for the matrix-vector kernel");
     const int nb = batch_depth(p, dtype, out);
-    if (out == OUT_QATTN && ((in != IN_NORM && in != IN_EMBED) || exact))  // the parallel-order attention's
-        return set_error(FG_ERR_SHAPE, "the query attention takes a normed row in parallel order");
+    if (out == OUT_QATTN && ((in != IN_NORM && in != IN_EMBED) || (exact && (in != IN_NORM || !p.scores))))
+        return set_error(FG_ERR_SHAPE, "the query attention takes a normed row (in the exact order, and its scores' buffer)");
     return dtype == FG_Q4B32 ? launch_proj_q4(p, in, out, exact, nb, smem, grid, s)
                              : launch_proj_q8(p, in, out, exact, nb, smem, grid, s);
 }

@@ -78,6 +78,8 @@ struct ProjParams {
     // chunk's record to `states`; the rest project the key and value rows in rotary pairs
     int per_chunk;
     float *states;
+    // ... in the exact order, the chunk's scores instead: [heads][capacity]
+    float *scores;
 };
 
 // a / b for 0 <= a < 2^22 and b >= 1 from rcp = fl(1/b): (a + 1/2)/b is at least 1/(2b) from
@@ -140,5 +142,6 @@ __device__ __forceinline__ float ref_silu(float x) { return x / (1.0f + ref_exp(
 
 size_t proj_smem(const ProjParams &p, int rows, int in, int out);
 int launch_proj(const ProjParams &p, int dtype, int in, int out, bool exact, hipStream_t s);
+int launch_norm_quantize(const ProjParams &p, bool exact, hipStream_t s);
 
 }  // namespace fg

@@ -400,8 +400,9 @@ __device__ __forceinline__ void value_slot(int lane, int wave, int &key0, int &d
     }
 }
 
-// The tile of keys j0 .. j0 + n - 1 of KV head `kv` (branch-free: keys past n re-read key j0).
-template <int D>
+// The tile of keys j0 .. j0 + n - 1 of KV head `kv` (branch-free: keys past n re-read key j0);
+// KEYS: the keys alone (the exact scores).
+template <int D, bool KEYS = false>
 __device__ __forceinline__ void load_kv_tile(const ProjParams &p, int kv, int j0, int n, KVTile<D> &t)
 {
     if (D == 0) return;
@@ -412,6 +413,7 @@ __device__ __forceinline__ void load_kv_tile(const ProjParams &p, int kv, int j0
     const unsigned koff = unsigned((jk < n ? jk : 0) * D + part * S::DQ);
 #pragma unroll
     for (int i = 0; i < S::DQ / 4; i++) t.k[i] = *reinterpret_cast<const v4f *>(kt + (koff + 4u * i));
+    if (KEYS) return;
     int key0, dim0;
     value_slot<D>(lane, wave, key0, dim0);
 #pragma unroll
@@ -506,6 +508,48 @@ __device__ __forceinline__ void attend_chunk(const ProjParams &p, const float *q
             rec[0] = M;
             rec[1] = L;
         }
+    }
+}
+
+// The exact order's scores of chunk c of query head h (ops.rs:310-326): for each key j in
+// [c·per_chunk, min((c + 1)·per_chunk, position)), dot_f32(q, k_j) in index order from −0, times
+// 1/√D, into scores[h][j]. The four lanes of a key hold a quarter of its dimensions each, in order:
+// the quarters' products are added one quarter after another, each lane continuing the sum that
+// the previous quarter's lane passes on. The first tile is already in `tile`.
+template <int D>
+__device__ __forceinline__ void score_chunk(const ProjParams &p, const float *qrot, int h, int c, KVTile<D> &tile)
+{
+    if (D == 0) return;
+    using S = AttnShape<D>;
+    const int tid = threadIdx.x, lane = tid & 63, jk = tid >> 2, part = tid & 3;
+    const int kv = divq(h, p.rcp_group);
+    const int first = c * p.per_chunk, last = min(p.position, first + p.per_chunk);
+    v4f q[S::DQ / 4 > 0 ? S::DQ / 4 : 1];
+#pragma unroll
+    for (int i = 0; i < S::DQ / 4; i++) q[i] = *reinterpret_cast<const v4f *>(qrot + part * S::DQ + 4 * i);
+    const float scale = 1.0f / sqrtf(float(D));
+    float *out = p.scores + size_t(h) * p.capacity;
+    for (int j0 = first; j0 < last; j0 += kTileKeys) {
+        const int n = min(kTileKeys, last - j0);
+        if (j0 != first) load_kv_tile<D, true>(p, kv, j0, n, tile);
+        v4f prod[S::DQ / 4 > 0 ? S::DQ / 4 : 1];
+#pragma unroll
+        for (int i = 0; i < S::DQ / 4; i++) prod[i] = q[i] * tile.k[i];
+        float s = -0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            // every lane continues from quarter t − 1's sum; quarter t's lane holds the real one
+            float run = s;
+#pragma unroll
+            for (int i = 0; i < S::DQ / 4; i++) {
+                run = run + prod[i].x;
+                run = run + prod[i].y;
+                run = run + prod[i].z;
+                run = run + prod[i].w;
+            }
+            s = __shfl(run, (lane & ~3) | t, 64);
+        }
+        if (part == 0 && jk < n) out[j0 + jk] = s * scale;
     }
 }
 
@@ -752,7 +796,8 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         head = divq(unit, p.rcp_chunks);
         chunk = unit - head * p.chunks;
         const int first = chunk * p.per_chunk;
-        load_kv_tile<HD>(p, divq(head, p.rcp_group), first, max(0, min(kTileKeys, min(p.position, first + p.per_chunk) - first)), tile);
+        load_kv_tile<HD, EXACT>(p, divq(head, p.rcp_group), first,
+                                max(0, min(kTileKeys, min(p.position, first + p.per_chunk) - first)), tile);
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (kDouble) {
@@ -872,7 +917,8 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
             }
         }
         __syncthreads();
-        attend_chunk<HD>(p, qrot, head, chunk, tile, qrot + HD);
+        if (EXACT) score_chunk<HD>(p, qrot, head, chunk, tile);
+        else attend_chunk<HD>(p, qrot, head, chunk, tile, qrot + HD);
     } else if (OUT == OUT_QKV || OUT == OUT_QATTN) {
         // a rotary pair per workgroup (qstride = D/8, qpw = 2): outputs 0..3 are dimensions
         // j0..j0+3 of a head, outputs 4..7 the same dimensions + D/2. The bias is in; query and key

@@ -26,30 +26,32 @@ int dispatch_depth(const ProjParams &p, bool exact, int depth, size_t smem, unsi
     }
 }
 
-// The query workgroups stream a whole head (D rows): one batch of up to 16 chunks per wave.
-template <int FMT, int IN, int HD>
+// The query workgroups stream a whole head (D rows): one batch of up to 16 chunks per wave. In
+// the exact order (a normed row) they write their chunk's scores instead of attending over it.
+template <int FMT, int IN, int HD, bool EXACT>
 int dispatch_qattn_depth(const ProjParams &p, int depth, size_t smem, unsigned grid, hipStream_t s)
 {
-    return depth <= 1 ? launch_one<FMT, 1, IN, OUT_QATTN, false, 1, true, HD>(p, smem, grid, s)
-                      : launch_one<FMT, 1, IN, OUT_QATTN, false, 16, true, HD>(p, smem, grid, s);
+    return depth <= 1 ? launch_one<FMT, 1, IN, OUT_QATTN, EXACT, 1, !EXACT, HD>(p, smem, grid, s)
+                      : launch_one<FMT, 1, IN, OUT_QATTN, EXACT, 16, !EXACT, HD>(p, smem, grid, s);
 }
 
 // The query heads of a normed row, or (IN_EMBED, the first layer) of a table row normed.
-template <int FMT, int IN>
+template <int FMT, int IN, bool EXACT>
 int dispatch_qattn_in(const ProjParams &p, int depth, size_t smem, unsigned grid, hipStream_t s)
 {
     switch (p.D) {
-    case 32: return dispatch_qattn_depth<FMT, IN, 32>(p, depth, smem, grid, s);
-    case 64: return dispatch_qattn_depth<FMT, IN, 64>(p, depth, smem, grid, s);
-    default: return dispatch_qattn_depth<FMT, IN, 128>(p, depth, smem, grid, s);
+    case 32: return dispatch_qattn_depth<FMT, IN, 32, EXACT>(p, depth, smem, grid, s);
+    case 64: return dispatch_qattn_depth<FMT, IN, 64, EXACT>(p, depth, smem, grid, s);
+    default: return dispatch_qattn_depth<FMT, IN, 128, EXACT>(p, depth, smem, grid, s);
     }
 }
 
 template <int FMT>
-int dispatch_qattn(const ProjParams &p, int in, int depth, size_t smem, unsigned grid, hipStream_t s)
+int dispatch_qattn(const ProjParams &p, int in, bool exact, int depth, size_t smem, unsigned grid, hipStream_t s)
 {
-    return in == IN_EMBED ? dispatch_qattn_in<FMT, IN_EMBED>(p, depth, smem, grid, s)
-                          : dispatch_qattn_in<FMT, IN_NORM>(p, depth, smem, grid, s);
+    if (exact) return dispatch_qattn_in<FMT, IN_NORM, true>(p, depth, smem, grid, s);
+    return in == IN_EMBED ? dispatch_qattn_in<FMT, IN_EMBED, false>(p, depth, smem, grid, s)
+                          : dispatch_qattn_in<FMT, IN_NORM, false>(p, depth, smem, grid, s);
 }
 
 template <int FMT>
@@ -72,7 +74,7 @@ int launch_proj_format(const ProjParams &p, int in, int out, bool exact, int nb,
     switch (out) {
     case OUT_QKV: return dispatch_depth<FMT, IN_NORM, OUT_QKV>(p, exact, nb, smem, grid, s);
     case OUT_SWIGLU: return dispatch_depth<FMT, IN_NORM, OUT_SWIGLU>(p, exact, nb, smem, grid, s);
-    case OUT_QATTN: return dispatch_qattn<FMT>(p, in, nb, smem, grid, s);
+    case OUT_QATTN: return dispatch_qattn<FMT>(p, in, exact, nb, smem, grid, s);
     default:
         if (in == IN_NORM) return dispatch_depth<FMT, IN_NORM, OUT_STORE>(p, exact, nb, smem, grid, s);
         if (in == IN_F32) return dispatch_depth<FMT, IN_F32, OUT_STORE>(p, exact, nb, smem, grid, s);

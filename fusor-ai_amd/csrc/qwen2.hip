@@ -2,25 +2,25 @@
 // Prediction::predict (blocks/src/transformer.rs:185-341, layer.rs:161-344,
 // layer/input.rs:22-66, lm.rs:97-179), every projection through the projection kernel.
 //
-// Per layer, each projection with its neighbours fused in. In the reference's order (exact), five
-// launches:
-//   1. RMSNorm + quantize -> QKV product + bias -> RoPE on query/key heads, keys and values kept
-//   2. attention of every query head over the cache, by head and 32 value dimensions: the scores,
-//      the softmax and the weighted values, quantized for the output projection (head sizes 64
-//      and 128; other sizes take two launches, the scores by key blocks and then the rest)
-//   3. output projection added to the residual row
-//   4. RMSNorm + quantize -> gate and up products -> silu(gate)·up, each workgroup's 32 outputs
+// Per layer, each projection with its neighbours fused in, four launches:
+//   1. RMSNorm + quantize -> QKV product + bias -> RoPE: every query head's rows recomputed by
+//      each of its chunk workgroups, which then take their chunk of the cached keys; the key and
+//      value rows of the position projected, rotated and kept by the remaining workgroups
+//   2. output projection added to the residual row, its input the attention row
+//   3. RMSNorm + quantize -> gate and up products -> silu(gate)·up, each workgroup's 32 outputs
 //      quantized as one group for down
-//   5. down projection added to the residual row
-// In parallel order, four: 1 and 2 become one launch whose workgroups each project one query head
-// and attend over one chunk of the cached keys (flash decoding), next to workgroups projecting the
-// position's key and value rows; the output projection's prologue merges the chunks with the new
-// key's own state.
-// then RMSNorm + quantize -> head product (logits) with per-workgroup greedy candidates, and the
-// greedy token. Elementwise arithmetic is the reference's operation for operation (no fused
-// multiply-add; ops::exp's polynomial). Reductions whose order changes f32 bits (RMSNorm's sum of
-// squares, the softmax total, the attention's weighted sum) run in the reference's index order when
-// the model is exact, or as parallel trees otherwise.
+//   4. down projection added to the residual row
+// In parallel order the chunk workgroups attend over their keys (flash decoding) and the output
+// projection's prologue merges the chunks with the new key's own state. In the reference's order
+// (exact) they write their keys' scores, and one more launch between 1 and 2 takes the attention
+// of every query head by head and 32 value dimensions: the new key's score, the softmax and the
+// weighted values in key order, quantized for the output projection (head sizes 64 and 128; other
+// sizes project QKV by rotary pairs and take the scores by key blocks in a launch of their own).
+// Then RMSNorm + quantize (one workgroup) -> head product (logits) with per-workgroup greedy
+// candidates, and the greedy token. Elementwise arithmetic is the reference's operation for
+// operation (no fused multiply-add; ops::exp's polynomial). Reductions whose order changes f32
+// bits (RMSNorm's sum of squares, the softmax total, the attention's weighted sum) run in the
+// reference's index order when the model is exact, or as parallel trees otherwise.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -302,32 +302,25 @@ __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
     return s;
 }
 
-// The exact-order attention of one query head for kWeighDims value dimensions in one launch (the
-// reference's arithmetic of attn_scores_kernel and attn_weigh_kernel<true>, ops.rs:301-342). Grid:
-// (heads, D / kWeighDims), 256 threads; every workgroup of a head forms the head's scores itself.
-// Every load is coalesced: neighbouring lanes read neighbouring 16 bytes of one key (or value)
-// row, and the rows' products reach the lane that adds them through LDS.
-//   scores: a wave takes a batch of 16·KPI keys (KPI = 256 / D rows per load), lane l holding
-//           piece l % (D/4) of rows l / (D/4) + KPI·e; it forms the products q·k of its pieces into
-//           its wave's LDS stage (row-major, each row's pieces rotated by the row so that the reads
-//           below spread over the banks), and lane r then adds row r's D products in index order
-//           from −0 (dot_f32), times 1/√D. Two batches per wave are in flight;
+// The exact-order attention of one query head for kWeighDims value dimensions (the reference's
+// arithmetic of attn_weigh_kernel<true>, ops.rs:301-342), over the scores of the cached keys that
+// the query launch formed (score_chunk). Grid: (heads, D / kWeighDims), 256 threads.
+//   scores: the cached keys' read back; the position's own key (the last) scored here: dot_f32 of
+//           the rotated query and the new key in index order from −0, times 1/√D;
 //   softmax: the maximum, w_j = ops::exp(s_j − max), their total from −0 in index order (one lane,
 //           reads running ahead of the additions: chain_sum), w_j / total;
 //   values: per chunk of 256 keys, lane l of a wave holds piece l % 8 (four dimensions) of rows
-//           l / 8 + 8·e and forms their products w_j·v_j[i] into LDS (a padded row per
-//           dimension, two buffers); lanes 0..31 of the first wave add their row to their output
-//           i in key order from +0 while the other waves form the next chunk's products. The
-//           value rows of the first two chunks are requested when the scores are done, so their
-//           latency hides under the softmax.
+//           l / 8 + 8·e (neighbouring lanes read neighbouring 16 bytes of a row) and forms their
+//           products w_j·v_j[i] into LDS (a padded row per dimension, two buffers); lanes 0..31
+//           of the first wave add their row to their output i in key order from +0 while the
+//           other waves form the next chunk's products. The value rows of the first two chunks
+//           are requested with the scores, so their latency hides under the softmax.
 // Then the 32 outputs are quantized as one group for the output projection.
 constexpr int kExactChunk = 256;
 constexpr int kProdRow = kExactChunk + 4;  // one dimension's products over a chunk, padded: the
                                           // lanes' 128-bit reads of their rows spread over the banks
-constexpr int kExactStage = 16384;         // bytes of one wave's batch of score products
-// the region after the weights: the four waves' score stages, then two buffers of value products
+// the region after the weights: two buffers of value products
 constexpr int kExactRegion = 2 * kWeighDims * kProdRow * 4;
-static_assert(4 * kExactStage <= kExactRegion, "exact region");
 
 inline size_t exact_attention_smem(size_t capacity) { return size_t((capacity + 15) / 16 * 16 + 16) * 4 + kExactRegion; }
 
@@ -335,30 +328,17 @@ template <int D>
 __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
 {
     extern __shared__ __align__(16) float ash[];
-    constexpr int PPL = D / 4;       // 16-byte pieces per key row
-    constexpr int KPI = 64 / PPL;    // key rows per wave load
-    constexpr int NI = 16;           // loads per batch
-    constexpr int BATCH = NI * KPI;  // keys per wave and batch (64 for D = 64, 32 for D = 128)
-    constexpr int STEP = 4 * BATCH;  // keys per workgroup and batch
-    static_assert(BATCH * D * 4 == kExactStage, "exact stage");
     const int keys = a.keys, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int head = blockIdx.x, d0 = int(blockIdx.y) * kWeighDims;
     const int kv = head / (a.heads / a.kv_heads);
     float *w = ash;                                     // [capacity] scores, then weights
     float *red = w + (a.capacity + 15) / 16 * 16;       // [16]
-    float *stage = red + 16 + wave * (BATCH * D);       // this wave's [BATCH][D] score products
     float *prod = red + 16;                             // [2][kWeighDims][kProdRow] value products
     const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
     const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D + d0;
-    const int piece = lane % PPL, krow = lane / PPL;  // this lane's piece and row of a key load
-    const int vpiece = lane & 7, vrow = lane >> 3;    // ... and of a value load (32 dimensions)
+    const int vpiece = lane & 7, vrow = lane >> 3;  // this lane's piece and row of a value load
     // (clamped re-reads past the last key: in bounds, never stored)
-    auto fetch_keys = [&](int j0, v4f *kr) {
-#pragma unroll
-        for (int e = 0; e < NI; e++)
-            kr[e] = *reinterpret_cast<const v4f *>(kbase + size_t(min(j0 + e * KPI + krow, keys - 1)) * D + 4 * piece);
-    };
     auto fetch_rows = [&](int c, v4f *v) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -366,70 +346,45 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
             v[e] = *reinterpret_cast<const v4f *>(vbase + size_t(j) * D + 4 * vpiece);
         }
     };
-    const v4f qp = *reinterpret_cast<const v4f *>(a.qkv + size_t(head) * D + 4 * piece);
-    v4f ka[NI], kb[NI];  // two batches of keys, named sets (a dynamically indexed pair spills)
-    fetch_keys(wave * BATCH, ka);
-    if (STEP < keys) fetch_keys(STEP + wave * BATCH, kb);
     const float scale = 1.0f / sqrtf(float(D));
     float local_max = -INFINITY;
-    // one batch: keys j0 .. j0 + BATCH - 1 of this wave
-    auto batch = [&](int j0, const v4f *kr) {
+    if (wave == 0) {
+        // the position's own key: lanes 4i .. 4i + 3 hold a quarter of the dimensions each, and
+        // the quarters' products are added one after another, each lane continuing the sum the
+        // previous quarter's lane passes on
+        constexpr int DQ = D / 4;
+        const int part = lane & 3;
+        const float *qh = a.qkv + size_t(head) * D + part * DQ;
+        const float *kn = kbase + size_t(keys - 1) * D + part * DQ;
+        v4f qk[DQ / 4];
 #pragma unroll
-        for (int e = 0; e < NI; e++) {
-            const int r = e * KPI + krow;
-            const v4f x = kr[e];
-            *reinterpret_cast<v4f *>(stage + r * D + 4 * (piece ^ (r & 15))) = v4f{qp.x * x.x, qp.y * x.y, qp.z * x.z, qp.w * x.w};
-        }
-        // a wave's LDS accesses complete in order: the writes above precede the reads below
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < BATCH) {
-            // the row's pieces in runs of eight, two register sets in turn (reads ahead)
-            const float *row = stage + lane * D;
-            constexpr int RUNS = PPL / 8;
-            v4f A[8], B[8];
-            auto load = [&](v4f *r, int g) {
+        for (int i = 0; i < DQ / 4; i++)
+            qk[i] = *reinterpret_cast<const v4f *>(qh + 4 * i) * *reinterpret_cast<const v4f *>(kn + 4 * i);
+        float s = -0.0f;
 #pragma unroll
-                for (int u = 0; u < 8; u++) r[u] = *reinterpret_cast<const v4f *>(row + 4 * ((8 * g + u) ^ (lane & 15)));
-            };
-            float s = -0.0f;  // dot_f32 in index order (arch/scalar.rs:340-342)
-            auto add = [&](const v4f *r) {
+        for (int t = 0; t < 4; t++) {
+            float run = s;
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    s = s + r[u].x;
-                    s = s + r[u].y;
-                    s = s + r[u].z;
-                    s = s + r[u].w;
-                }
-            };
-            load(A, 0);
-#pragma unroll
-            for (int g = 0; g < RUNS; g += 2) {
-                if (g + 1 < RUNS) load(B, g + 1);
-                __builtin_amdgcn_sched_barrier(0);
-                add(A);
-                if (g + 2 < RUNS) load(A, g + 2);
-                __builtin_amdgcn_sched_barrier(0);
-                if (g + 1 < RUNS) add(B);
+            for (int i = 0; i < DQ / 4; i++) {
+                run = run + qk[i].x;
+                run = run + qk[i].y;
+                run = run + qk[i].z;
+                run = run + qk[i].w;
             }
-            if (j0 + lane < keys) {
-                w[j0 + lane] = s * scale;
-                local_max = fmaxf(local_max, s * scale);
-            }
+            s = __shfl(run, (lane & ~3) | t, 64);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
-    for (int s0 = 0; s0 < keys; s0 += 2 * STEP) {
-        batch(s0 + wave * BATCH, ka);
-        if (s0 + 2 * STEP < keys) fetch_keys(s0 + 2 * STEP + wave * BATCH, ka);
-        if (s0 + STEP < keys) {
-            batch(s0 + STEP + wave * BATCH, kb);
-            if (s0 + 3 * STEP < keys) fetch_keys(s0 + 3 * STEP + wave * BATCH, kb);
+        if (lane == 0) {
+            w[keys - 1] = s * scale;
+            local_max = s * scale;
         }
     }
-    // the value rows of the first two chunks, requested only now: held across the scores they
-    // would take registers the keys need, and the softmax hides their latency
+    const float *sc = a.scores + size_t(head) * a.capacity;
+    for (int j = tid; j < keys - 1; j += kAttnThreads) {
+        const float v = sc[j];
+        w[j] = v;
+        local_max = fmaxf(local_max, v);
+    }
+    // the value rows of the first two chunks: the softmax hides their latency
     v4f va[8], vb[8];
     fetch_rows(0, va);
     if (kExactChunk < keys) fetch_rows(1, vb);
@@ -615,10 +570,16 @@ int qkv_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position
 // Whether the attention runs as flash decoding merged by the output projection (parallel order).
 bool fast_attention(const fg_qwen2 *m) { return !m->shape.exact && m->shape.heads * m->shape.head_dim <= 1024; }
 
+// Whether, in the exact order, the query launch forms the cached keys' scores and the attention
+// launch reads them (head sizes 64 and 128).
+bool prescored_attention(const fg_qwen2 *m) { return m->shape.exact && (m->shape.head_dim == 64 || m->shape.head_dim == 128); }
+
 // 1.-2. in parallel order, one launch: every query head's rows (RMSNorm + quantize -> product +
 // bias -> RoPE) recomputed by each of its chunk workgroups, which then attend over their chunk of
 // the cached keys [0, position); the key and value rows of the position projected, rotated and
 // kept by the remaining workgroups. The output projection merges the chunks with the new key.
+// In the exact order the same launch with the reference's sums, whose chunk workgroups write
+// their keys' scores for the attention launch instead of attending.
 int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t position, hipStream_t st, int token = -1)
 {
     const fg_qwen2_shape &sh = m->shape;
@@ -648,6 +609,7 @@ int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t positi
     p.chunks = m->chunks;
     p.per_chunk = m->per_chunk;
     p.states = m->part;
+    p.scores = m->scores;
     if (token >= 0) {
         // the first layer reads the token's table row itself (Buffers::embed_row, lm.rs:99-107)
         // and keeps it in hidden for the residual
@@ -659,7 +621,7 @@ int qattn_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, size_t li, size_t positi
         p.x_out = m->hidden;
         return launch_proj(p, sh.dtype, IN_EMBED, OUT_QATTN, false, st);
     }
-    return launch_proj(p, sh.dtype, IN_NORM, OUT_QATTN, false, st);
+    return launch_proj(p, sh.dtype, IN_NORM, OUT_QATTN, sh.exact != 0, st);
 }
 
 // 3. and 5. a projection added to the residual row: of the attention's output (o: quantized by
@@ -734,9 +696,8 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st, fl
     a.corr = m->xc;
     a.row_out = row_out;
     const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims));
-    if (sh.exact && (sh.head_dim == 64 || sh.head_dim == 128)) {
-        // one launch: the head's scores, softmax and ordered weighted sums (measured faster than
-        // the scores kernel followed by this kernel's softmax and sums alone)
+    if (prescored_attention(m)) {
+        // the cached keys' scores come from the query launch; the softmax and ordered weighted sums
         if (sh.head_dim == 64) attn_exact_kernel<64><<<wgrid, kAttnThreads, m->exact_smem, st>>>(a);
         else attn_exact_kernel<128><<<wgrid, kAttnThreads, m->exact_smem, st>>>(a);
         FG_HIP(hipGetLastError());
@@ -760,7 +721,8 @@ int run_layer(fg_qwen2 *m, size_t li, size_t position, hipStream_t st, int token
         if ((rc = qattn_launch(m, ly, li, position, st, token))) return rc;
         if ((rc = residual_launch(m, ly.o, IN_ATTN, st, li, position))) return rc;
     } else {
-        if ((rc = qkv_launch(m, ly, li, position, st))) return rc;
+        if ((rc = prescored_attention(m) ? qattn_launch(m, ly, li, position, st) : qkv_launch(m, ly, li, position, st)))
+            return rc;
         if ((rc = attention_launch(m, li, position, st))) return rc;
         if ((rc = residual_launch(m, ly.o, IN_PREQ, st))) return rc;
     }
@@ -772,16 +734,25 @@ int head_launch(fg_qwen2 *m, hipStream_t st)
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(m->table);
-    p.qpw = kHeadQuads;
     p.x = m->hidden;
     p.norm_w = m->final_norm;
     p.eps = sh.eps;
     p.zp = m->zp;
+    // the final norm's row formed once (not in each of the product's workgroups)
+    p.q_out = m->xq;
+    p.s_out = m->xs;
+    p.c_out = m->xc;
+    int rc = launch_norm_quantize(p, sh.exact != 0, st);
+    if (rc) return rc;
+    p.q = m->xq;
+    p.as = m->xs;
+    p.corr = m->xc;
+    p.qpw = kHeadQuads;
     p.out = m->logits;
     p.ld_out = long(m->table->quads * 4);
     p.pval = m->pval;
     p.pidx = m->pidx;
-    return launch_proj(p, sh.dtype, IN_NORM, OUT_STORE, sh.exact != 0, st);
+    return launch_proj(p, sh.dtype, IN_PREQ, OUT_STORE, sh.exact != 0, st);
 }
 
 bool table_is(const fg_table *t, int dtype, size_t rows, size_t cols)
@@ -924,7 +895,8 @@ extern "C" int fg_qwen2_attention(fg_qwen2 *m, size_t layer, size_t position, co
         if ((rc = qattn_launch(m, ly, layer, position, st))) return rc;
         if ((rc = residual_launch(m, ly.o, IN_ATTN, st, layer, position, row))) return rc;
     } else {
-        if ((rc = qkv_launch(m, ly, layer, position, st))) return rc;
+        if ((rc = prescored_attention(m) ? qattn_launch(m, ly, layer, position, st) : qkv_launch(m, ly, layer, position, st)))
+            return rc;
         if ((rc = attention_launch(m, layer, position, st, row))) return rc;
     }
     FG_HIP(hipMemcpyAsync(query, m->qkv, sh.heads * sh.head_dim * 4, hipMemcpyDeviceToDevice, st));

@@ -94,6 +94,8 @@ int launch_proj(const ProjParams &p0, int dtype, int in, int out, bool exact, hi
     proj_derive(p);
     const int span = p.qstride * p.qpw;
     if (p.qstride > 1 && (nq % span || p.qpw != 2)) return set_error(FG_ERR_SHAPE, "strided quads come in whole pairs");
+    if (p.pval && (out != OUT_STORE || p.qpw > 16 || p.qstride != 1))
+        return set_error(FG_ERR_SHAPE, "greedy candidates take at most 16 consecutive quads per workgroup");
     if (out == OUT_QKV && (p.qpw != 2 || p.qstride * 8 != p.D))
         return set_error(FG_ERR_SHAPE, "the QKV epilogue takes one rotary pair per workgroup");
     if (out == OUT_SWIGLU && p.q_out && (p.qpw != 8 || p.qstride != 1 || nq % 8))

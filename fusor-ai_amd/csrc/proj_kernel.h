@@ -858,42 +858,20 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
 
     if (OUT == OUT_STORE) {
         if (p.pval) {
-            // this workgroup's greedy candidate (lm.rs:169-179): the first largest, NaN never wins
+            // this workgroup's greedy candidate (lm.rs:169-179): the first largest, NaN never wins.
+            // Its outputs (at most 64, checked on the host) are one per lane of the first wave in
+            // column order: the wave's maximum (NaN ignored), then the first lane holding it.
             __syncthreads();
-            float best = 0.0f;
-            int idx = -1;
-            for (int nl = threadIdx.x; nl < nq * 4; nl += kThreads) {
-                const int n = output_of(nl);
-                const float v = ybuf[nl];
-                if (n < p.n_rows && v == v && (idx < 0 || v > best)) {
-                    best = v;
-                    idx = n;
+            if (wave == 0) {
+                float v = __builtin_nanf("");
+                if (lane < nq * 4 && output_of(lane) < p.n_rows) v = ybuf[lane];
+                const float best = wave_allmax(v);
+                const unsigned long long hit = __ballot(v == best);
+                const int first = hit ? __ffsll((long long)hit) - 1 : 0;
+                if (lane == first) {
+                    p.pval[blockIdx.x] = hit ? v : 0.0f;
+                    p.pidx[blockIdx.x] = hit ? output_of(lane) : -1;
                 }
-            }
-            for (int m = 32; m >= 1; m >>= 1) {
-                const float ob = __shfl_xor(best, m, 64);
-                const int oi = __shfl_xor(idx, m, 64);
-                if (oi >= 0 && (idx < 0 || ob > best || (ob == best && oi < idx))) {
-                    best = ob;
-                    idx = oi;
-                }
-            }
-            if (lane == 0) {
-                red[wave] = best;
-                reinterpret_cast<int *>(red)[8 + wave] = idx;
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                for (int w = 1; w < kThreads / 64; w++) {
-                    const float ob = red[w];
-                    const int oi = reinterpret_cast<int *>(red)[8 + w];
-                    if (oi >= 0 && (idx < 0 || ob > best || (ob == best && oi < idx))) {
-                        best = ob;
-                        idx = oi;
-                    }
-                }
-                p.pval[blockIdx.x] = best;
-                p.pidx[blockIdx.x] = idx;
             }
         }
         return;

@@ -191,8 +191,8 @@ def test_layer_forward_equals_the_oracle_layer(fk):
 
 @pytest.mark.parametrize("exact", [True, False])
 def test_consecutive_steps_feed_back_the_greedy_token(fk, exact):
-    """Several steps on one model, each fed the previous step's greedy token: the head's last
-    workgroup picks the token and resets its count for the next step. Exact mode matches the
+    """Several steps on one model, each fed the previous step's greedy token (the head's
+    workgroups leave one candidate each, a last launch picks among them). Exact mode matches the
     oracle's tokens and cache rows step by step; parallel order repeats its own first step."""
     import torch
     dtype = O.Q7B32
@@ -218,6 +218,70 @@ def test_consecutive_steps_feed_back_the_greedy_token(fk, exact):
         again, _, _ = gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact)
         again.step(5, 4, next_token=nxt)
         assert int(host(nxt)[0]) == firsts[0]
+
+
+def first_largest(logits):
+    """Prediction::greedy (lm.rs:169-179): the first index of the largest logit, NaNs never win,
+    and a NaN first logit keeps index 0."""
+    best, idx = logits[0], 0
+    for i in range(1, len(logits)):
+        if logits[i] > best:
+            best, idx = logits[i], i
+    return idx
+
+
+@pytest.mark.parametrize("exact", [True, False])
+@pytest.mark.parametrize("start", [5, 300])
+def test_greedy_pick_takes_the_first_of_equal_logits_and_never_a_nan(fk, exact, start):
+    """The greedy token with ties and NaNs placed in the head's table (64 rows per workgroup of
+    candidates): the largest row a copied to row a // 2 (the same workgroup for a small a, another
+    for a large one), a NaN scale on row a // 2 instead, and a NaN scale on row 0. Exact mode
+    matches the oracle's token; both modes pick the reference's token from their own logits."""
+    import torch
+    dtype = O.Q7B32
+    shape = dict(SMALL, vocab=700)  # 175 quads: 11 workgroups of candidates
+    sh, lys, final, table, kc, vc = build(dtype, seed=12, synthetic=False, **shape)
+    rng = np.random.default_rng(12)
+    rows = rng.standard_normal((sh.vocab, sh.hidden)).astype(np.float32)
+    base = O.encode(dtype, sh.vocab, sh.hidden, rows)
+    # a token whose own (embedding) row none of the changes touches (the tied table makes a token's
+    # own row its largest logit, as here)
+    for token in range(start, start + 40):
+        _, _, a = O.Qwen2(sh, lys, final, base).step(kc.copy(), vc.copy(), token, 9, threads=8)
+        if a > 1 and token != a // 2:
+            break
+    else:
+        pytest.fail("no token leaves its own row unchanged")
+    b = a // 2
+    tied = rows.copy()
+    tied[b] = rows[a]
+    quant_len = (sh.vocab + 3) // 4 * 4 * sh.hidden  # Q7b32: a byte per code; the scales follow
+    groups = sh.hidden // 32
+
+    def nan_scale(t, row):
+        t = t.copy()
+        at = quant_len + ((row // 4 * groups) * 4 + row % 4) * 4  # the row's first group
+        t[at:at + 4] = np.frombuffer(np.float32(np.nan).tobytes(), np.uint8)
+        return t
+
+    cases = {"tie": (O.encode(dtype, sh.vocab, sh.hidden, tied), b), "nan_earlier": (nan_scale(base, b), a),
+             "nan_first": (nan_scale(base, 0), 0)}
+    for name, (t, expect) in cases.items():
+        model, _, _ = gpu_model(fk, dtype, sh, lys, final, t, kc, vc, exact)
+        logits = torch.empty(sh.vocab, dtype=torch.float32, device="cuda")
+        nxt = torch.empty(1, dtype=torch.int32, device="cuda")
+        model.step(token, 9, logits=logits, next_token=nxt)
+        got, got_l = int(host(nxt)[0]), host(logits)
+        assert got == first_largest(got_l), name
+        if name == "tie":
+            assert same_bits(got_l[a], got_l[b]) and got != a, name
+        elif name == "nan_earlier":
+            assert np.isnan(got_l[b]) and got != b, name
+        else:
+            assert np.isnan(got_l[0]) and got == 0, name
+        if exact:
+            _, _, want = O.Qwen2(sh, lys, final, t).step(kc.copy(), vc.copy(), token, 9, threads=8)
+            assert got == want == expect, name
 
 
 def test_decoder_rejects_positions_past_the_cache(fk):

@@ -111,6 +111,27 @@ __device__ __forceinline__ int sum8(int v)
 }
 // Maximum / sum over the wave of a value every lane holds, every lane getting the result: DPP
 // within rows of 16 lanes, then lane exchanges across the rows (no scalar round trips).
+// Lane C of each row of 16 lanes, to every lane of its row (DPP row_newbcast).
+template <int C>
+__device__ __forceinline__ float row_broadcast_of(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + C, 0xF, 0xF, false));
+}
+// ... for a lane index that is a constant where the call is unrolled (0..7)
+__device__ __forceinline__ float row_broadcast(float x, int c)
+{
+    switch (c) {
+    case 0: return row_broadcast_of<0>(x);
+    case 1: return row_broadcast_of<1>(x);
+    case 2: return row_broadcast_of<2>(x);
+    case 3: return row_broadcast_of<3>(x);
+    case 4: return row_broadcast_of<4>(x);
+    case 5: return row_broadcast_of<5>(x);
+    case 6: return row_broadcast_of<6>(x);
+    default: return row_broadcast_of<7>(x);
+    }
+}
+
 __device__ __forceinline__ float wave_allmax(float v)
 {
     v = fmaxf(v, __int_as_float(xor1(__float_as_int(v))));

@@ -161,8 +161,9 @@ __device__ __forceinline__ void stage_issue(const ProjParams &p, StageRegs &g)
 #pragma unroll
         for (int c = 0; c < kMaxChunks; c++) {
             const float *rec = p.part + size_t(h * p.chunks + min(c, p.chunks - 1)) * (p.D + 4);
-            g.pm[c] = rec[0];
-            g.pl[c] = rec[1];
+            const float2 ml = *reinterpret_cast<const float2 *>(rec);  // the maximum and total
+            g.pm[c] = ml.x;
+            g.pl[c] = ml.y;
             g.pa[c] = *reinterpret_cast<const v4f *>(rec + 4 + d4);
         }
     } else if (IN == IN_EMBED) {
@@ -286,19 +287,22 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         for (int c = 0; c < kMaxChunks; c++)
             if (c < p.chunks) M = fmaxf(M, g.pm[c]);
         const float en = ref_exp(sn - M);
-        // e^(m_c − M) once per head: lane c of the head's D/4 lanes (at least 8) takes chunk c,
-        // and every lane of the head reads them back in chunk order
+        // e^(m_c − M) once per head and row of 16 lanes: lane c of the row (D >= 64: a head fills
+        // whole rows) or of the head's D/4 = 8 lanes (D = 32) takes chunk c, and every lane of the
+        // head reads them back in chunk order, by a row broadcast or a lane shuffle
         const int head0 = (tid & 63) & ~((p.D >> 2) - 1);
+        const bool rows = p.D >= 64;
+        const int slot = rows ? (tid & 15) : (tid & 63) - head0;
         float mine = 0.0f;
 #pragma unroll
         for (int c = 0; c < kMaxChunks; c++)
-            if ((tid & 63) - head0 == c) mine = g.pm[c];
-        const float e_mine = (tid & 63) - head0 < p.chunks ? ref_exp(mine - M) : 0.0f;
+            if (slot == c) mine = g.pm[c];
+        const float e_mine = slot < p.chunks ? ref_exp(mine - M) : 0.0f;
         float L = en;
         v4f o = g.vn * en;
 #pragma unroll
         for (int c = 0; c < kMaxChunks; c++) {
-            const float e = __shfl(e_mine, head0 + c, 64);
+            const float e = rows ? row_broadcast(e_mine, c) : __shfl(e_mine, head0 + c, 64);
             if (c < p.chunks) {
                 L = L + g.pl[c] * e;
                 o = o + g.pa[c] * e;

@@ -109,8 +109,26 @@ __device__ __forceinline__ int sum8(int v)
     v += xor2(v);
     return v + mirror8(v);
 }
-// Maximum / sum over the wave of a value every lane holds, every lane getting the result: DPP
-// within rows of 16 lanes, then lane exchanges across the rows (no scalar round trips).
+// The value of lane l ^ 8 within its row of 16 lanes (DPP row_ror:8).
+__device__ __forceinline__ float xor8(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+// The two rows of 16 lanes that lane l's row pairs with (lanes l and l ^ 16), at l's place in its
+// row: .x the even row's value, .y the odd row's. A VALU lane swap (v_permlane16_swap), so
+// x + y, or fmaxf(x, y), is the xor-16 exchange with the same operands in both lanes.
+__device__ __forceinline__ float2 row_pair(float v)
+{
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+// ... and the two halves of 32 lanes (lanes l and l ^ 32): .x the lower half's, .y the upper's
+__device__ __forceinline__ float2 half_pair(float v)
+{
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 // Lane C of each row of 16 lanes, to every lane of its row (DPP row_newbcast).
 template <int C>
 __device__ __forceinline__ float row_broadcast_of(float x)
@@ -132,23 +150,29 @@ __device__ __forceinline__ float row_broadcast(float x, int c)
     }
 }
 
+// Maximum / sum over the wave of a value every lane holds, every lane getting the result: DPP
+// within rows of 16 lanes, then lane swaps across the rows (no LDS or scalar round trips).
 __device__ __forceinline__ float wave_allmax(float v)
 {
     v = fmaxf(v, __int_as_float(xor1(__float_as_int(v))));
     v = fmaxf(v, __int_as_float(xor2(__float_as_int(v))));
     v = fmaxf(v, __int_as_float(mirror8(__float_as_int(v))));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));  // row_ror:8
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    v = fmaxf(v, xor8(v));
+    const float2 r = row_pair(v);
+    v = fmaxf(r.x, r.y);
+    const float2 h = half_pair(v);
+    return fmaxf(h.x, h.y);
 }
 __device__ __forceinline__ float wave_allsum(float v)
 {
     v = v + __int_as_float(xor1(__float_as_int(v)));
     v = v + __int_as_float(xor2(__float_as_int(v)));
     v = v + __int_as_float(mirror8(__float_as_int(v)));
-    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
-    v = v + __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
+    v = v + xor8(v);
+    const float2 r = row_pair(v);
+    v = r.x + r.y;
+    const float2 h = half_pair(v);
+    return h.x + h.y;
 }
 
 // Activation quantization of one value at scale d (scalar.rs:57-66): ties-to-even rounding of the

@@ -280,7 +280,11 @@ __device__ __forceinline__ void stage_finish(const ProjParams &p, const StageReg
         sn = sn + __int_as_float(xor1(__float_as_int(sn)));
         sn = sn + __int_as_float(xor2(__float_as_int(sn)));
         sn = sn + __int_as_float(mirror8(__float_as_int(sn)));
-        for (int w = 8; w < p.D / 4; w <<= 1) sn = sn + __shfl_xor(sn, w, 64);
+        if (p.D >= 64) sn = sn + xor8(sn);
+        if (p.D >= 128) {
+            const float2 r = row_pair(sn);
+            sn = r.x + r.y;
+        }
         sn = sn * (1.0f / sqrtf(float(p.D)));
         float M = sn;
 #pragma unroll
@@ -852,7 +856,15 @@ __global__ __launch_bounds__(kThreads) void proj_kernel(ProjParams p)
         if (team >= 2) s = s + __int_as_float(xor1(__float_as_int(s)));
         if (team >= 4) s = s + __int_as_float(xor2(__float_as_int(s)));
         if (team >= 8) s = s + __int_as_float(mirror8(__float_as_int(s)));
-        for (int m = 8; m < team; m <<= 1) s = s + __shfl_xor(s, m, 64);
+        if (team >= 16) s = s + xor8(s);
+        if (team >= 32) {
+            const float2 r = row_pair(s);
+            s = r.x + r.y;
+        }
+        if (team >= 64) {
+            const float2 h = half_pair(s);
+            s = h.x + h.y;
+        }
         if (sub == 0 && live(my_out)) finish(my_out, s);
     } else {
         // group order: the reference's sequential sum, one thread per (table, row, output)

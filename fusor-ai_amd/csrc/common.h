@@ -129,6 +129,23 @@ __device__ __forceinline__ float2 half_pair(float v)
     return make_float2(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
+// Lane C of each quad of lanes, to every lane of its quad (DPP quad_perm [C, C, C, C]).
+template <int C>
+__device__ __forceinline__ float quad_broadcast_of(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), C * 0x55, 0xF, 0xF, false));
+}
+// ... for a lane index that is a constant where the call is unrolled (0..3)
+__device__ __forceinline__ float quad_broadcast(float x, int c)
+{
+    switch (c) {
+    case 0: return quad_broadcast_of<0>(x);
+    case 1: return quad_broadcast_of<1>(x);
+    case 2: return quad_broadcast_of<2>(x);
+    default: return quad_broadcast_of<3>(x);
+    }
+}
+
 // Lane C of each row of 16 lanes, to every lane of its row (DPP row_newbcast).
 template <int C>
 __device__ __forceinline__ float row_broadcast_of(float x)

@@ -555,7 +555,7 @@ __device__ __forceinline__ void score_chunk(const ProjParams &p, const float *qr
                 run = run + prod[i].z;
                 run = run + prod[i].w;
             }
-            s = __shfl(run, (lane & ~3) | t, 64);
+            s = quad_broadcast(run, t);
         }
         if (part == 0 && jk < n) out[j0 + jk] = s * scale;
     }

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnParams a)
 
 __device__ float attn_block_max(float v, float *red)
 {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    v = wave_allmax(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -127,7 +127,7 @@ __device__ float attn_block_max(float v, float *red)
 
 __device__ float attn_block_sum(float v, float *red)
 {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    v = wave_allsum(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = v;
     __syncthreads();
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
                 run = run + qk[i].z;
                 run = run + qk[i].w;
             }
-            s = __shfl(run, (lane & ~3) | t, 64);
+            s = quad_broadcast(run, t);
         }
         if (lane == 0) {
             w[keys - 1] = s * scale;

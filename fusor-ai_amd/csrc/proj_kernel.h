@@ -487,7 +487,10 @@ __device__ __forceinline__ void attend_chunk(const ProjParams &p, const float *q
             for (int i = 0; i < S::VPL; i++) acc[i] = acc[i] + w * tile.v[S::VPL * e + i];
         }
     }
-    if (D < 64) acc[0] = acc[0] + __shfl_xor(acc[0], 32, 64);  // the two halves' keys, same dims
+    if (D < 64) {
+        const float2 h = half_pair(acc[0]);  // the two halves' keys, same dims
+        acc[0] = h.x + h.y;
+    }
     // the waves' states merged: M = max m_w, L = Σ l_w·e^(m_w − M), acc = Σ acc_w·e^(m_w − M)
     float *wm = scratch, *wl = scratch + 4, *wacc = scratch + 8;  // [4], [4], [4][D]
     if (lane == 0) {

@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
         m = fmaxf(m, i + 2 < keys ? x.z : -INFINITY);
         m = fmaxf(m, i + 3 < keys ? x.w : -INFINITY);
     }
-    for (int s = 32; s >= 1; s >>= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+    m = wave_allmax(m);
     if (lane == 0) wmax[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
@@ -293,7 +293,7 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
         }
 #pragma unroll
         for (int o = 0; o < 8; o++) {
-            const float po = __shfl(part, o, 64);
+            const float po = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), o));
             if (lane == 0) total = total + po;
         }
         if (lane == 0) sums[r] = total;

@@ -373,16 +373,25 @@ struct Shape {
     }
 };
 
+// (image, head) units per batch of the weighted values' product: as many as keep their
+// exponentials' levels, scales and corrections within 512 MiB, at least one.
+size_t units_per_batch(const Shape &s)
+{
+    const size_t per = s.queries * s.pk + 2 * s.queries * (s.pk / 32) * 4;
+    return std::max<size_t>(1, std::min<size_t>(s.qtables, (size_t(512) << 20) / per));
+}
+
 // The call's scratch, carved from one allocation of the product's stream-ordered workspace pool:
 // no allocation reaches the driver and nothing waits for the stream. The key and value matrices
 // of every (image, key head) and the quantized queries of every (image, head) are built up front;
-// the scores, their levels and the products' outputs are per head.
+// the scores are per head, their levels per batch of heads, the products' outputs per call.
 struct Scratch {
     enum { KEYT, MEAN, KCODES, KSCALES, VCODES, VSCALES, QLEVELS, QSCALES, QCORR, QTSCALES, PROD, ELEVELS, ESCALES, ECORR, SUMS, PV, N };
     size_t size[N];
     void *part[N];
     explicit Scratch(const Shape &s)
     {
+        const size_t batch = units_per_batch(s);
         size[KEYT] = s.ktables * s.hd * s.kpad * 4;
         size[MEAN] = s.ktables * s.hd * 4;
         size[KCODES] = s.ktables * s.kquads * (s.pd / 32) * 128;
@@ -393,8 +402,8 @@ struct Scratch {
         size[QSCALES] = size[QCORR] = s.qtables * s.queries * (s.pd / 32) * 4;
         size[QTSCALES] = s.queries % 128 == 0 ? size[QSCALES] : 0;  // block-major, whole tiles of rows only
         size[PROD] = s.queries * s.keys4 * 4;
-        size[ELEVELS] = s.queries * s.pk;
-        size[ESCALES] = size[ECORR] = s.queries * (s.pk / 32) * 4;
+        size[ELEVELS] = batch * s.queries * s.pk;
+        size[ESCALES] = size[ECORR] = batch * s.queries * (s.pk / 32) * 4;
         size[SUMS] = s.qtables * s.queries * 4;
         size[PV] = s.qtables * s.queries * s.hd * 4;
     }
@@ -442,53 +451,61 @@ int run(const fg_attention *c, float *out, hipStream_t st, const Shape &s, const
         s.queries % 128 == 0 ? w.at<float>(Scratch::QTSCALES) : nullptr);
     FG_HIP(hipGetLastError());
     int rc;
-    for (size_t image = 0; image < c->images; image++) {
-        for (size_t kh = 0; kh < c->kv_heads; kh++) {
-            const size_t t = image * c->kv_heads + kh;
-            fg_table ktab = runtime_matrix(w.at<int8_t>(Scratch::KCODES) + t * s.kquads * (s.pd / 32) * 128,
-                                           w.at<float>(Scratch::KSCALES) + t * s.kquads * (s.pd / 32) * 4, s.keys, s.pd);
-            fg_table vtab = runtime_matrix(w.at<int8_t>(Scratch::VCODES) + t * s.vquads * (s.pk / 32) * 128,
-                                           w.at<float>(Scratch::VSCALES) + t * s.vquads * (s.pk / 32) * 4, s.hd, s.pk);
-            for (size_t h = kh * group; h < (kh + 1) * group; h++) {
-                // Scratch::unit (attention.rs:157-214) for every query of the image at once
-                const size_t u = image * c->heads + h;
-                ProductArgs a{};
-                a.t = &ktab;
-                a.q = w.at<int8_t>(Scratch::QLEVELS) + u * s.queries * s.pd;
-                a.as = w.at<float>(Scratch::QSCALES) + u * s.queries * (s.pd / 32);
-                a.corr = w.at<int32_t>(Scratch::QCORR) + u * s.queries * (s.pd / 32);
-                if (s.queries % 128 == 0) {
-                    a.as_t = w.at<float>(Scratch::QTSCALES) + u * s.queries * (s.pd / 32);
-                    a.as_t_rows = s.queries;
-                }
-                a.rows = s.queries;
-                a.quad_begin = 0;
-                a.quad_end = size_t(keys4 / 4);
-                a.out = w.at<float>(Scratch::PROD);
-                a.ld_out = size_t(keys4);
-                if ((rc = launch_product(a, st))) return rc;
-                float *sums = w.at<float>(Scratch::SUMS) + u * s.queries;
-                rc = c->exponentials == FG_EXP_FAST
-                         ? launch_exponentials<true>(w.at<float>(Scratch::PROD), keys4, scale, keys, pk,
-                                                     w.at<int8_t>(Scratch::ELEVELS), w.at<float>(Scratch::ESCALES),
-                                                     w.at<int32_t>(Scratch::ECORR), sums, unsigned(queries), st)
-                         : launch_exponentials<false>(w.at<float>(Scratch::PROD), keys4, scale, keys, pk,
-                                                      w.at<int8_t>(Scratch::ELEVELS), w.at<float>(Scratch::ESCALES),
-                                                      w.at<int32_t>(Scratch::ECORR), sums, unsigned(queries), st);
-                if (rc) return rc;
-                ProductArgs b{};
-                b.t = &vtab;
-                b.q = w.at<int8_t>(Scratch::ELEVELS);
-                b.as = w.at<float>(Scratch::ESCALES);
-                b.corr = w.at<int32_t>(Scratch::ECORR);
-                b.rows = s.queries;
-                b.quad_begin = 0;
-                b.quad_end = size_t(hd / 4);
-                b.out = w.at<float>(Scratch::PV) + u * s.queries * s.hd;
-                b.ld_out = s.hd;
-                if ((rc = launch_product(b, st))) return rc;
+    // Scratch::unit (attention.rs:157-214) for every query of an (image, head) unit at once: unit
+    // u = image · heads + h reads key head table t = u / group. Per unit the scores' product and
+    // the exponentials (into the unit's slice of the batch's levels); per batch of units the
+    // weighted values' products in one launch.
+    const size_t batch = units_per_batch(s), elev = s.queries * s.pk, escl = s.queries * (s.pk / 32);
+    const size_t kcode = s.kquads * (s.pd / 32) * 128, kscl = s.kquads * (s.pd / 32) * 4;
+    const size_t vcode = s.vquads * (s.pk / 32) * 128, vscl = s.vquads * (s.pk / 32) * 4;
+    for (size_t u0 = 0; u0 < s.qtables; u0 += batch) {
+        const size_t u1 = std::min(s.qtables, u0 + batch);
+        for (size_t u = u0; u < u1; u++) {
+            const size_t t = u / group;
+            fg_table ktab = runtime_matrix(w.at<int8_t>(Scratch::KCODES) + t * kcode, w.at<float>(Scratch::KSCALES) + t * kscl,
+                                           s.keys, s.pd);
+            ProductArgs a{};
+            a.t = &ktab;
+            a.q = w.at<int8_t>(Scratch::QLEVELS) + u * s.queries * s.pd;
+            a.as = w.at<float>(Scratch::QSCALES) + u * s.queries * (s.pd / 32);
+            a.corr = w.at<int32_t>(Scratch::QCORR) + u * s.queries * (s.pd / 32);
+            if (s.queries % 128 == 0) {
+                a.as_t = w.at<float>(Scratch::QTSCALES) + u * s.queries * (s.pd / 32);
+                a.as_t_rows = s.queries;
             }
+            a.rows = s.queries;
+            a.quad_begin = 0;
+            a.quad_end = size_t(keys4 / 4);
+            a.out = w.at<float>(Scratch::PROD);
+            a.ld_out = size_t(keys4);
+            if ((rc = launch_product(a, st))) return rc;
+            float *sums = w.at<float>(Scratch::SUMS) + u * s.queries;
+            int8_t *lev = w.at<int8_t>(Scratch::ELEVELS) + (u - u0) * elev;
+            float *lsc = w.at<float>(Scratch::ESCALES) + (u - u0) * escl;
+            int32_t *lco = w.at<int32_t>(Scratch::ECORR) + (u - u0) * escl;
+            rc = c->exponentials == FG_EXP_FAST
+                     ? launch_exponentials<true>(w.at<float>(Scratch::PROD), keys4, scale, keys, pk, lev, lsc, lco, sums,
+                                                 unsigned(queries), st)
+                     : launch_exponentials<false>(w.at<float>(Scratch::PROD), keys4, scale, keys, pk, lev, lsc, lco, sums,
+                                                  unsigned(queries), st);
+            if (rc) return rc;
         }
+        // the weighted values of every unit of the batch: unit u's levels times value table u / group
+        const size_t t0 = u0 / group;
+        fg_table vtab = runtime_matrix(w.at<int8_t>(Scratch::VCODES) + t0 * vcode, w.at<float>(Scratch::VSCALES) + t0 * vscl,
+                                       s.hd, s.pk);
+        ProductArgs b{};
+        b.t = &vtab;
+        b.q = w.at<int8_t>(Scratch::ELEVELS);
+        b.as = w.at<float>(Scratch::ESCALES);
+        b.corr = w.at<int32_t>(Scratch::ECORR);
+        b.rows = s.queries;
+        b.quad_begin = 0;
+        b.quad_end = size_t(hd / 4);
+        b.out = w.at<float>(Scratch::PV) + u0 * s.queries * s.hd;
+        b.ld_out = s.hd;
+        if ((rc = launch_gemm_batch(b, int(u1 - u0), int(group), int(u0 % group), elev, escl, s.queries * s.hd, vcode, vscl, st)))
+            return rc;
     }
     // each output divided by its row's sum, every head at once
     const size_t n = s.qtables * s.queries * s.hd;

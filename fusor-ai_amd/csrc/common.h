@@ -440,6 +440,11 @@ size_t product_scratch_bytes(const ProductArgs &a);
 hipError_t workspace_alloc(void **ptr, size_t bytes, hipStream_t s);
 int launch_matvec(const ProductArgs &a, hipStream_t s);
 int launch_gemm(const ProductArgs &a, hipStream_t s);
+// `items` products of pre-quantized rows of one shape in one launch (the staged kernel): item z's
+// levels, scales and outputs at z times the strides (elements) from a's, and its table's codes
+// and scales (z + first) / per_table − first / per_table tables on from a.t's.
+int launch_gemm_batch(const ProductArgs &a, int items, int per_table, int first, size_t q_stride, size_t as_stride,
+                      size_t out_stride, size_t codes_stride, size_t scales_stride, hipStream_t s);
 int launch_t2(const ProductArgs &a, hipStream_t s);
 int launch_product(const ProductArgs &a, hipStream_t s);
 }  // namespace fg

@@ -45,6 +45,10 @@ struct GemmParams {
     int accumulate;
     int32_t *dots;
     int dots_cols;
+    // a batch of products (the staged kernel's grid y): item z takes the levels, scales and outputs
+    // z items on (strides in elements) and table z / per_table's codes and scales
+    long q_batch, as_batch, out_batch, codes_batch, wscales_batch;
+    int per_table, first;  // item z's table: (z + first) / per_table − first / per_table on
 };
 
 // Workgroups in launch order go round-robin to the 8 XCDs, each with its own L2, so neighbouring
@@ -818,6 +822,14 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p)
     constexpr int BM = T::BM, BN = T::BN, KB = T::KB, RB = T::RB;
     constexpr int QB = FMT == 8 ? 128 : 64;  // device bytes per quad block
     extern __shared__ __align__(16) unsigned char stage_lds[];  // [2][STAGE]
+    if (gridDim.y > 1) {  // item blockIdx.y of a batch
+        const long z = blockIdx.y, zt = (z + p.first) / p.per_table - p.first / p.per_table;
+        p.q += z * p.q_batch;
+        p.as += z * p.as_batch;
+        p.out += z * p.out_batch;
+        p.codes += zt * p.codes_batch;
+        p.wscales += zt * p.wscales_batch;
+    }
     const int tid = threadIdx.x, lane = tid & 63, i = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int tx, ty;
@@ -1257,6 +1269,43 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
     }
     return rc;
+}
+
+int launch_gemm_batch(const ProductArgs &a, int items, int per_table, int first, size_t q_stride, size_t as_stride,
+                      size_t out_stride, size_t codes_stride, size_t scales_stride, hipStream_t s)
+{
+    const fg_table *t = a.t;
+    if (items < 1 || per_table < 1 || first < 0 || !a.q || !a.as || a.x || a.dots || a.fused || a.accumulate || a.as_t || a.bias ||
+        (t->dtype != FG_Q7B32 && t->dtype != FG_Q8B32) || a.rows < 1 || a.quad_end <= a.quad_begin)
+        return set_error(FG_ERR_ARG, "a batch of products takes pre-quantized rows and a Q7b32 or Q8b32 table");
+    if (items > 65535) return set_error(FG_ERR_SHAPE, "at most 65535 products in a batch");
+    GemmParams p{};
+    p.codes = t->codes;
+    p.wscales = t->scales;
+    p.B = int(t->blocks);
+    p.G = int(t->groups);
+    p.K = int(t->cols);
+    p.M = int(a.rows);
+    p.Mpad = int((a.rows + 127) / 128 * 128);
+    p.col_begin = int(a.quad_begin * 4);
+    p.col_end = int(a.quad_end * 4);
+    p.n_rows = int(t->rows);
+    p.q = a.q;
+    p.as = a.as;
+    p.out = a.out;
+    p.ld_out = long(a.ld_out);
+    p.q_batch = long(q_stride);
+    p.as_batch = long(as_stride);
+    p.out_batch = long(out_stride);
+    p.codes_batch = long(codes_stride);
+    p.wscales_batch = long(scales_stride);
+    p.per_table = per_table;
+    p.first = first;
+    using T = LdsTile<8, 1, 1>;
+    const long groups = long((p.col_end - p.col_begin + T::BN - 1) / T::BN) * ((p.M + T::BM - 1) / T::BM);
+    gemm_lds_kernel<8, 1, 1, false><<<dim3(unsigned(groups), unsigned(items)), 256, 2 * size_t(T::STAGE), s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
 }
 
 int launch_gemm(const ProductArgs &a, hipStream_t s)

@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 namespace fg {
 namespace {
@@ -374,11 +375,17 @@ struct Shape {
 };
 
 // (image, head) units per batch of the weighted values' product: as many as keep their
-// exponentials' levels, scales and corrections within 512 MiB, at least one.
+// exponentials' levels, scales and corrections within 512 MiB, at least one. FG_ATTEND_UNITS
+// sets a smaller batch, for tests of the batches' edges.
 size_t units_per_batch(const Shape &s)
 {
     const size_t per = s.queries * s.pk + 2 * s.queries * (s.pk / 32) * 4;
-    return std::max<size_t>(1, std::min<size_t>(s.qtables, (size_t(512) << 20) / per));
+    size_t n = std::max<size_t>(1, std::min<size_t>(s.qtables, (size_t(512) << 20) / per));
+    if (const char *env = getenv("FG_ATTEND_UNITS")) {
+        const long v = atol(env);
+        if (v >= 1) n = std::min(n, size_t(v));
+    }
+    return n;
 }
 
 // The call's scratch, carved from one allocation of the product's stream-ordered workspace pool:

@@ -47,13 +47,14 @@ def same_bits(a, b):
 
 
 CASES = [  # heads, kv_heads, head_dim, images, queries, keys, fast
-    (2, 2, 64, 1, 3, 200, True),      # 3 query rows: the matrix-vector kernel
-    (6, 1, 32, 3, 5, 9, True),        # 5 rows: the 16-row matrix-core kernel
+    (2, 2, 64, 1, 3, 200, True),      # 3 query rows: the scores on the matrix-vector kernel
+    (6, 1, 32, 3, 5, 9, True),        # 5 rows: the scores on the 16-row matrix-core kernel
     (4, 2, 40, 2, 37, 53, False),     # 37 rows, padded head_dim (40 -> 64) and keys (53 -> 64)
     (4, 2, 40, 2, 37, 53, True),
     (3, 3, 16, 1, 1, 1, False),       # one key, one query
-    (8, 2, 128, 1, 64, 1000, False),  # a long row of keys
-    (1, 1, 64, 1, 4, 4096, True),     # the DiT block's 4096 keys, on the matrix-vector kernel
+    (8, 2, 128, 1, 64, 1000, False),  # a long row of keys; 128 value channels: 128-wide tiles
+    (2, 1, 72, 1, 70, 300, True),     # the DiT block's head size: 72 channels in one 128-wide tile
+    (1, 1, 64, 1, 4, 4096, True),     # the DiT block's 4096 keys, the scores on the matrix-vector kernel
     (2, 1, 64, 1, 5, 16384, False),   # the largest row of keys: 64 KiB of scores per row in LDS
     (1, 1, 32, 1, 2, 16384, True),
 ]
@@ -69,6 +70,22 @@ def test_attend_is_the_oracles_bits(fk, case):
     v = rng.standard_normal((I * K, KV * D)).astype(np.float32)
     want = O.attend(H, KV, D, I, Q, K, q, k, v, fast=fast)
     got = gpu_attend(fk, H, KV, D, I, Q, K, q, k, v, fast)
+    assert same_bits(got, want), np.max(np.abs(got - want))
+
+
+@pytest.mark.parametrize("units", [1, 4, 5])
+def test_attend_in_batches_of_heads(fk, monkeypatch, units):
+    """The weighted values' product runs per batch of (image, head) units, each unit reading key
+    head table unit / group; batches of 1, 4 and 5 units over 2 images of 6 heads in 2 key heads
+    start at every offset into a key head's group."""
+    H, KV, D, I, Q, K = 6, 2, 72, 2, 37, 53
+    monkeypatch.setenv("FG_ATTEND_UNITS", str(units))
+    rng = np.random.default_rng(units)
+    q = rng.standard_normal((I * Q, H * D)).astype(np.float32)
+    k = rng.standard_normal((I * K, KV * D)).astype(np.float32)
+    v = rng.standard_normal((I * K, KV * D)).astype(np.float32)
+    want = O.attend(H, KV, D, I, Q, K, q, k, v, fast=True)
+    got = gpu_attend(fk, H, KV, D, I, Q, K, q, k, v, True)
     assert same_bits(got, want), np.max(np.abs(got - want))
 
 

@@ -119,34 +119,56 @@ __device__ __forceinline__ void clear_block(int8_t *codes32, float *scale)
     *scale = 0.0f;
 }
 
+// Q7b32 levels of four values at scale d (quant.rs:143-150: rne(x / d) clamped to ±63 through the
+// saturating cast), packed as one dword of device levels.
+__device__ __forceinline__ int q7_levels4(const float (&x)[4], float d)
+{
+    int l[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float v = __builtin_rintf(x[j] / d);
+        const int level = v != v ? 0 : v >= 127.0f ? 127 : v <= -128.0f ? -128 : int(v);
+        l[j] = level < -63 ? -63 : (level > 63 ? 63 : level);
+    }
+    return pack4(l[0], l[1], l[2], l[3]);
+}
+
 // Scratch::quantize's key matrices (attention.rs:100-118) for every (image, key head) at once:
 // row k of table t is key[k] − mean over the channels, zeros to the padded width; rows past the
-// keys to the quad are cleared. One thread per (table, row, block).
-__global__ void key_table_kernel(const float *__restrict__ key, size_t stride, size_t offset, int kv_heads, int keys,
-                                 int hd, int rows4, int blocks, const float *__restrict__ mean, int8_t *__restrict__ codes,
-                                 float *__restrict__ scales, size_t tables)
+// keys to the quad are cleared. Eight aligned lanes per (table, row, block), four channels each,
+// the block's largest magnitude by lane exchanges (q7_block's arithmetic). Indices in 32 bits:
+// the host keeps the lane count below 2^31.
+__global__ __launch_bounds__(256) void key_table_kernel(const float *__restrict__ key, size_t stride, size_t offset,
+                                                        int kv_heads, int keys, int hd, int rows4, int blocks,
+                                                        const float *__restrict__ mean, int8_t *__restrict__ codes,
+                                                        float *__restrict__ scales, unsigned groups)
 {
-    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (id >= tables * rows4 * blocks) return;
-    const int b = int(id % blocks), row = int(id / blocks % rows4);
-    const size_t t = id / (size_t(blocks) * rows4);
-    const size_t tb = (t * (rows4 / 4) + row / 4) * blocks + b;  // quad block of the tables' run
-    int8_t *dst = codes + tb * 128 + (row % 4) * 32;
+    const unsigned lid = blockIdx.x * 256u + threadIdx.x, sub = lid & 7u;
+    const unsigned g = min(lid >> 3, groups - 1);  // past the end: the last group again, never stored
+    const unsigned b = g % unsigned(blocks), rb = g / unsigned(blocks), row = rb % unsigned(rows4),
+                   t = rb / unsigned(rows4);
+    const size_t tb = (size_t(t) * unsigned(rows4 / 4) + row / 4) * unsigned(blocks) + b;  // quad block of the tables' run
+    int *dst = reinterpret_cast<int *>(codes + tb * 128 + (row % 4) * 32);
     float *scale = scales + tb * 4 + row % 4;
-    if (row >= keys) {
-        clear_block(dst, scale);
-        return;
-    }
-    const size_t image = t / kv_heads, kh = t % kv_heads;
-    const float *src = key + (image * size_t(keys) + row) * stride + offset + kh * size_t(hd);
-    const float *mu = mean + t * hd;
-    float x[32];
+    const bool live = int(row) < keys;
+    const unsigned image = t / unsigned(kv_heads), kh = t % unsigned(kv_heads);
+    const float *src = key + (size_t(image) * unsigned(keys) + min(int(row), keys - 1)) * stride + offset + size_t(kh) * hd;
+    const float *mu = mean + size_t(t) * hd;
+    float x[4];
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const int d = 32 * b + i;
-        x[i] = d < hd ? src[d] - mu[d] : 0.0f;
+    for (int j = 0; j < 4; j++) {
+        const int d = 32 * int(b) + 4 * int(sub) + j;
+        x[j] = d < hd ? src[d] - mu[d] : 0.0f;
     }
-    *scale = q7_block(x, reinterpret_cast<int *>(dst));
+    float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    amax = max8(fmaxf(0.0f, amax));
+    const float d = group_scale(amax, 63.0f);
+    const int packed = q7_levels4(x, d);
+    if ((lid >> 3) >= groups) return;
+    // rows past the keys: the cleared block (QuantizedMatrix::extend's padding rows), zero codes
+    // (device levels −64) and a zero scale
+    dst[sub] = live ? packed : int(0xC0C0C0C0u);
+    if (sub == 0) *scale = live ? d : 0.0f;
 }
 
 // Scratch::quantize's value matrices (Scratch::transpose, attention.rs:119-137) for every
@@ -155,25 +177,25 @@ __global__ void key_table_kernel(const float *__restrict__ key, size_t stride, s
 // fastest so neighbouring threads read neighbouring channels.
 __global__ void value_table_kernel(const float *__restrict__ value, size_t stride, size_t offset, int kv_heads,
                                    int keys, int hd, int rows4, int blocks, int8_t *__restrict__ codes,
-                                   float *__restrict__ scales, size_t tables)
+                                   float *__restrict__ scales, unsigned n)
 {
-    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (id >= tables * rows4 * blocks) return;
-    const int row = int(id % rows4), b = int(id / rows4 % blocks);
-    const size_t t = id / (size_t(blocks) * rows4);
-    const size_t tb = (t * (rows4 / 4) + row / 4) * blocks + b;
+    const unsigned id = blockIdx.x * blockDim.x + threadIdx.x;  // 32-bit: the host keeps n below 2^31
+    if (id >= n) return;
+    const int row = int(id % unsigned(rows4));
+    const unsigned rb = id / unsigned(rows4), b = rb % unsigned(blocks), t = rb / unsigned(blocks);
+    const size_t tb = (size_t(t) * unsigned(rows4 / 4) + row / 4) * unsigned(blocks) + b;
     int8_t *dst = codes + tb * 128 + (row % 4) * 32;
     float *scale = scales + tb * 4 + row % 4;
     if (row >= hd) {
         clear_block(dst, scale);
         return;
     }
-    const size_t image = t / kv_heads, kh = t % kv_heads;
-    const float *src = value + image * size_t(keys) * stride + offset + kh * size_t(hd) + row;
+    const unsigned image = t / unsigned(kv_heads), kh = t % unsigned(kv_heads);
+    const float *src = value + size_t(image) * unsigned(keys) * stride + offset + size_t(kh) * hd + row;
     float x[32];
 #pragma unroll
     for (int i = 0; i < 32; i++) {
-        const int k = 32 * b + i;
+        const int k = 32 * int(b) + i;
         x[i] = k < keys ? src[size_t(k) * stride] : 0.0f;
     }
     *scale = q7_block(x, reinterpret_cast<int *>(dst));
@@ -186,26 +208,27 @@ __global__ void value_table_kernel(const float *__restrict__ value, size_t strid
 // Eight lanes per group of 32.
 __global__ __launch_bounds__(256) void query_levels_kernel(const float *__restrict__ query, size_t stride,
                                                            size_t offset, int heads, int queries, int hd, int pd,
-                                                           size_t slots, int8_t *__restrict__ levels,
+                                                           unsigned slots, int8_t *__restrict__ levels,
                                                            float *__restrict__ lscales, int32_t *__restrict__ lcorr,
                                                            float *__restrict__ tscales)
 {
-    const size_t id = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int per_row = pd / 4;
+    const unsigned id = blockIdx.x * blockDim.x + threadIdx.x;  // 32-bit: the host keeps slots below 2^31
+    const unsigned per_row = unsigned(pd / 4);
     const bool active = id < slots;
     const int s4 = int(id % per_row);
-    const size_t rr = id / per_row;  // u · queries + r
-    const size_t u = rr / queries, r = rr % queries;
+    const unsigned rrq = id / per_row;  // u · queries + r
+    const size_t rr = rrq;
+    const unsigned u = rrq / unsigned(queries), r = rrq % unsigned(queries);
     v4f v{0.0f, 0.0f, 0.0f, 0.0f};
     if (active && 4 * s4 < hd) {
-        const size_t image = u / heads, h = u % heads;
-        const float *src = query + (image * size_t(queries) + r) * stride + offset + h * size_t(hd) + 4 * s4;
+        const unsigned image = u / unsigned(heads), h = u % unsigned(heads);
+        const float *src = query + (size_t(image) * unsigned(queries) + r) * stride + offset + size_t(h) * hd + 4 * s4;
         v = v4f{src[0], src[1], src[2], src[3]};
     }
     Group8 gr[1];
     quantize_groups<1>(&v, gr);
     if (active) store_group8(gr[0], 64, s4 / 8, levels + rr * pd, lscales + rr * (pd / 32), lcorr + rr * (pd / 32));
-    if (tscales && active && (threadIdx.x & 7) == 0) tscales[(u * (pd / 32) + s4 / 8) * size_t(queries) + r] = gr[0].d;
+    if (tscales && active && (threadIdx.x & 7) == 0) tscales[(size_t(u) * (pd / 32) + s4 / 8) * unsigned(queries) + r] = gr[0].d;
 }
 
 // One workgroup of four waves per query row; thread t holds slots t, t + 256, ... (S of them, four
@@ -304,13 +327,13 @@ __global__ __launch_bounds__(256) void exponentials_kernel(const float *__restri
 // out[(image · queries + r) · stride + h · hd + d] = pv[u][r][d] / sums[u][r] for every (image,
 // head) u = image · heads + h.
 __global__ void divide_kernel(const float *__restrict__ pv, const float *__restrict__ sums, int heads, int queries,
-                              int hd, size_t n, float *__restrict__ out, size_t stride)
+                              int hd, unsigned n, float *__restrict__ out, size_t stride)
 {
-    const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;  // 32-bit: the host keeps n below 2^31
     if (i >= n) return;
-    const size_t ur = i / hd, u = ur / queries, r = ur % queries, image = u / heads, h = u % heads;
-    const int d = int(i % hd);
-    out[(image * queries + r) * stride + h * hd + d] = pv[i] / sums[ur];
+    const unsigned ur = i / unsigned(hd), u = ur / unsigned(queries), r = ur % unsigned(queries);
+    const unsigned image = u / unsigned(heads), h = u % unsigned(heads), d = i - ur * unsigned(hd);
+    out[(size_t(image) * unsigned(queries) + r) * stride + size_t(h) * hd + d] = pv[i] / sums[ur];
 }
 
 unsigned blocks_for(size_t n) { return unsigned((n + kThreads - 1) / kThreads); }
@@ -444,16 +467,16 @@ int run(const fg_attention *c, float *out, hipStream_t st, const Shape &s, const
                                                 w.at<float>(Scratch::KEYT));
     key_mean_kernel<<<unsigned(s.ktables * s.hd), 64, size_t((kpad + 4095) / 4096 * 4096) * 4, st>>>(
         w.at<float>(Scratch::KEYT), keys, kpad, w.at<float>(Scratch::MEAN));
-    const size_t kthreads = s.ktables * s.kquads * 4 * (s.pd / 32), vthreads = s.ktables * s.vquads * 4 * (s.pk / 32);
-    key_table_kernel<<<blocks_for(kthreads), kThreads, 0, st>>>(
+    const size_t kgroups = s.ktables * s.kquads * 4 * (s.pd / 32), vthreads = s.ktables * s.vquads * 4 * (s.pk / 32);
+    key_table_kernel<<<blocks_for(8 * kgroups), kThreads, 0, st>>>(
         c->key, c->key_stride, c->key_offset, int(c->kv_heads), keys, hd, int(s.kquads * 4), pd / 32,
-        w.at<float>(Scratch::MEAN), w.at<int8_t>(Scratch::KCODES), w.at<float>(Scratch::KSCALES), s.ktables);
+        w.at<float>(Scratch::MEAN), w.at<int8_t>(Scratch::KCODES), w.at<float>(Scratch::KSCALES), unsigned(kgroups));
     value_table_kernel<<<blocks_for(vthreads), kThreads, 0, st>>>(
         c->value, c->value_stride, c->value_offset, int(c->kv_heads), keys, hd, int(s.vquads * 4), pk / 32,
-        w.at<int8_t>(Scratch::VCODES), w.at<float>(Scratch::VSCALES), s.ktables);
+        w.at<int8_t>(Scratch::VCODES), w.at<float>(Scratch::VSCALES), unsigned(vthreads));
     const size_t slots = s.qtables * s.queries * (s.pd / 4);
     query_levels_kernel<<<blocks_for(slots), kThreads, 0, st>>>(
-        c->query, c->query_stride, c->query_offset, int(c->heads), queries, hd, pd, slots,
+        c->query, c->query_stride, c->query_offset, int(c->heads), queries, hd, pd, unsigned(slots),
         w.at<int8_t>(Scratch::QLEVELS), w.at<float>(Scratch::QSCALES), w.at<int32_t>(Scratch::QCORR),
         s.queries % 128 == 0 ? w.at<float>(Scratch::QTSCALES) : nullptr);
     FG_HIP(hipGetLastError());
@@ -517,7 +540,7 @@ int run(const fg_attention *c, float *out, hipStream_t st, const Shape &s, const
     // each output divided by its row's sum, every head at once
     const size_t n = s.qtables * s.queries * s.hd;
     divide_kernel<<<blocks_for(n), kThreads, 0, st>>>(w.at<float>(Scratch::PV), w.at<float>(Scratch::SUMS), int(c->heads),
-                                                      queries, hd, n, out, stride);
+                                                      queries, hd, unsigned(n), out, stride);
     FG_HIP(hipGetLastError());
     return FG_OK;
 }
@@ -547,8 +570,12 @@ extern "C" int fg_attend(const fg_attention *c, float *out, void *stream)
         c->key_offset + c->kv_heads * c->head_dim > c->key_stride ||
         c->value_offset + c->kv_heads * c->head_dim > c->value_stride)
         return set_error(FG_ERR_SHAPE, "fg_attend: an operand's heads run past its row stride");
-    const hipStream_t st = static_cast<hipStream_t>(stream);
     const Shape s(c);
+    // the preparation and division kernels index their lanes in 32 bits
+    const size_t lanes = std::max({8 * s.ktables * s.kquads * 4 * (s.pd / 32), s.ktables * s.vquads * 4 * (s.pk / 32),
+                                   s.qtables * s.queries * (s.pd / 4), s.qtables * s.queries * s.hd});
+    if (lanes >= (size_t(1) << 31)) return set_error(FG_ERR_SHAPE, "fg_attend: at most 2^31 - 1 values of queries, keys or outputs");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
     Scratch w(s);
     void *ws = nullptr;
     FG_HIP(workspace_alloc(&ws, w.total(), st));

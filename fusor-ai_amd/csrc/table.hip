@@ -302,21 +302,21 @@ namespace {
 __global__ void quantize_rows_t_kernel(const float *__restrict__ x, size_t groups, int G, size_t Mpad, int8_t *__restrict__ q,
                                        float *__restrict__ as_t)
 {
-    const size_t t = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const size_t g = t / 8;
+    const unsigned t = blockIdx.x * blockDim.x + threadIdx.x;  // 32-bit: the host keeps the lanes below 2^31
+    const unsigned g = t / 8;
     const int sub = int(t % 8);
     const bool active = g < groups;
-    const float4 v = active ? reinterpret_cast<const float4 *>(x)[g * 8 + sub] : make_float4(0, 0, 0, 0);
+    const float4 v = active ? reinterpret_cast<const float4 *>(x)[size_t(g) * 8 + sub] : make_float4(0, 0, 0, 0);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = max8(fmaxf(0.0f, amax));
     int l0, l1, l2, l3;
     const float d = scale_and_levels(amax, v.x, v.y, v.z, v.w, l0, l1, l2, l3);
-    const size_t r = g / G, gi = g % G;
+    const unsigned r = g / unsigned(G), gi = g - r * unsigned(G);
     if (active) {
-        reinterpret_cast<int *>(q)[g * 8 + sub] = pack4(l0, l1, l2, l3);
-        if (sub == 0) as_t[gi * Mpad + r] = d;
+        reinterpret_cast<int *>(q)[size_t(g) * 8 + sub] = pack4(l0, l1, l2, l3);
+        if (sub == 0) as_t[size_t(gi) * Mpad + r] = d;
     } else if (r < Mpad && sub == 0) {
-        as_t[gi * Mpad + r] = 0.0f;
+        as_t[size_t(gi) * Mpad + r] = 0.0f;
     }
 }
 
@@ -328,6 +328,7 @@ int launch_quantize_rows_t(const float *x, size_t rows, size_t K, int dtype, int
     if (group_of(dtype) != 32) return set_error(FG_ERR_FORMAT, "block-major scales take groups of 32");
     const size_t G = K / 32, groups = rows * G, threads = Mpad * G * 8;
     if (threads == 0) return FG_OK;
+    if (threads >= (size_t(1) << 31)) return set_error(FG_ERR_SHAPE, "at most 2^31 - 1 quantization lanes in one launch");
     quantize_rows_t_kernel<<<unsigned((threads + 255) / 256), 256, 0, s>>>(x, groups, int(G), Mpad, q, as_t);
     FG_HIP(hipGetLastError());
     return FG_OK;

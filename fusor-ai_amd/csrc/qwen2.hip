@@ -309,14 +309,15 @@ __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
 //           the rotated query and the new key in index order from −0, times 1/√D;
 //   softmax: the maximum, w_j = ops::exp(s_j − max), their total from −0 in index order (one lane,
 //           reads running ahead of the additions: chain_sum), w_j / total;
-//   values: per chunk of 256 keys, lane l of a wave holds piece l % 8 (four dimensions) of rows
-//           l / 8 + 8·e (neighbouring lanes read neighbouring 16 bytes of a row) and forms their
-//           products w_j·v_j[i] into LDS (a padded row per dimension, two buffers); lanes 0..31
-//           of the first wave add their row to their output i in key order from +0 while the
-//           other waves form the next chunk's products. The value rows of the first two chunks
-//           are requested with the scores, so their latency hides under the softmax.
+//   values: per chunk of 192 keys, lane l of waves 1..3 holds piece l % 8 (four dimensions) of
+//           rows l / 8 + 8·e of its 64 (neighbouring lanes read neighbouring 16 bytes of a row)
+//           and forms their products w_j·v_j[i] into LDS (a padded row per dimension, two
+//           buffers); lanes 0..31 of the first wave add their row to their output i in key order
+//           from +0 while the other waves form the next chunk's products, so the first wave's
+//           additions run back to back. The value rows of the first two chunks are requested
+//           with the scores, so their latency hides under the softmax.
 // Then the 32 outputs are quantized as one group for the output projection.
-constexpr int kExactChunk = 256;
+constexpr int kExactChunk = 192;  // three waves of 64 rows
 constexpr int kProdRow = kExactChunk + 4;  // one dimension's products over a chunk, padded: the
                                           // lanes' 128-bit reads of their rows spread over the banks
 // the region after the weights: two buffers of value products
@@ -338,11 +339,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
     const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
     const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D + d0;
     const int vpiece = lane & 7, vrow = lane >> 3;  // this lane's piece and row of a value load
+    const int pw = wave - 1;                         // the product waves 1..3: 64 rows of a chunk each
     // (clamped re-reads past the last key: in bounds, never stored)
     auto fetch_rows = [&](int c, v4f *v) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const int j = min(c * kExactChunk + wave * 64 + 8 * e + vrow, keys - 1);
+            const int j = min(c * kExactChunk + pw * 64 + 8 * e + vrow, keys - 1);
             v[e] = *reinterpret_cast<const v4f *>(vbase + size_t(j) * D + 4 * vpiece);
         }
     };
@@ -386,8 +388,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
     }
     // the value rows of the first two chunks: the softmax hides their latency
     v4f va[8], vb[8];
-    fetch_rows(0, va);
-    if (kExactChunk < keys) fetch_rows(1, vb);
+    if (wave > 0) {
+        fetch_rows(0, va);
+        if (kExactChunk < keys) fetch_rows(1, vb);
+    }
     const float peak = attn_block_max(local_max, red);  // its barriers publish the scores
     for (int j = tid; j < keys; j += kAttnThreads) w[j] = ref_exp(w[j] - peak);
     __syncthreads();
@@ -404,12 +408,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
         float wj[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const int r = wave * 64 + 8 * e + vrow;
+            const int r = pw * 64 + 8 * e + vrow;
             wj[e] = r < n ? w[j0 + r] : 0.0f;
         }
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            float *col = buf + 4 * vpiece * kProdRow + wave * 64 + 8 * e + vrow;
+            float *col = buf + 4 * vpiece * kProdRow + pw * 64 + 8 * e + vrow;
             col[0] = wj[e] * v[e].x;
             col[kProdRow] = wj[e] * v[e].y;
             col[2 * kProdRow] = wj[e] * v[e].z;
@@ -417,21 +421,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
         }
     };
     // Step k: after the barrier chunk k's products are whole and chunk k - 1's sums are done, so
-    // every wave forms chunk k + 1's products into the other buffer (and requests chunk k + 3 into
+    // waves 1..3 form chunk k + 1's products into the other buffer (and request chunk k + 3 into
     // the freed registers) while lanes 0..31 of wave 0 add chunk k's.
     const int chunks = (keys + kExactChunk - 1) / kExactChunk;
     float *const buf0 = prod, *const buf1 = prod + kWeighDims * kProdRow;
     auto step = [&](int k, v4f *vnext, float *bnext, const float *bcur) {
         __syncthreads();
-        if (k + 1 < chunks) {
+        if (wave > 0 && k + 1 < chunks) {
             products(k + 1, vnext, bnext);
             if (k + 3 < chunks) fetch_rows(k + 3, vnext);
         }
         if (tid < kWeighDims) o = chain_sum(o, min(kExactChunk, keys - k * kExactChunk), bcur + tid * kProdRow);
     };
     __syncthreads();  // the weights
-    products(0, va, buf0);
-    if (2 < chunks) fetch_rows(2, va);
+    if (wave > 0) {
+        products(0, va, buf0);
+        if (2 < chunks) fetch_rows(2, va);
+    }
     for (int k = 0; k < chunks; k += 2) {
         step(k, vb, buf1, buf0);
         if (k + 1 < chunks) step(k + 1, va, buf0, buf1);

@@ -37,7 +37,7 @@ INT8_PEAK_TOPS = 5000.0
 VALU_LANE_OPS = 256 * 4 * 16 * 2.4e9
 METRIC = "int8 qmatvec weight GB/s (% HBM peak); Qwen2-0.5B-shape decode tokens/sec"
 
-Q7B32, Q4B32, Q8B32 = 1, 2, 4
+Q7B32, Q4B32, T2B128, Q8B32 = 1, 2, 3, 4
 
 
 def measured_traffic():
@@ -136,16 +136,20 @@ def cpu_product_baseline(np, dtype, n, k, table_bytes, x, rate, unit, sample):
 
 def synthetic_table(np, dtype, rows, cols, rng):
     """Reference bytes of a [rows, cols] table: i.i.d. codes (Q7b32 levels uniform in [-63, 63],
-    Q8b32 in [-127, 127], Q4b32 nibbles) and scales uniform in [1e-3, 1e-2]. rows % 4 == 0."""
+    Q8b32 in [-127, 127], Q4b32 nibbles, T2b128 ternary codes 0-2 in each two bits) and scales
+    uniform in [1e-3, 1e-2]. rows % 4 == 0."""
     assert rows % 4 == 0
-    n_codes = rows * cols // (2 if dtype == Q4B32 else 1)
+    n_codes = rows * cols // {Q4B32: 2, T2B128: 4}.get(dtype, 1)
     if dtype == Q7B32:
         codes = rng.integers(1, 128, n_codes, dtype=np.uint8)
     elif dtype == Q8B32:
         codes = rng.integers(-127, 128, n_codes, dtype=np.int16).astype(np.int8).view(np.uint8)
+    elif dtype == T2B128:
+        parts = rng.integers(0, 3, (n_codes, 4), dtype=np.uint8)
+        codes = (parts[:, 0] | parts[:, 1] << 2 | parts[:, 2] << 4 | parts[:, 3] << 6).astype(np.uint8)
     else:
         codes = rng.integers(0, 256, n_codes, dtype=np.uint8)
-    scales = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    scales = rng.uniform(1e-3, 1e-2, rows * cols // (128 if dtype == T2B128 else 32)).astype(np.float32)
     return np.concatenate([codes, scales.view(np.uint8)])
 
 
@@ -496,6 +500,23 @@ def extras(fk, torch, np, with_cpu=True):
             entry["cpu_baseline"] = cpu_product_baseline(np, Q4B32, n, k, data, xh, lambda ms_: b / ms_ / 1e6, "GB/s",
                                                          f"the whole product, {rows} f32 row(s) quantized first")
         res[f"int4_14336x4096_rows{rows}"] = entry
+    # 3b. ternary T2b128 14336 x 4096 (2 bits a weight, a scale per 128), rows 1 and 16
+    data = synthetic_table(np, T2B128, n, k, rng)
+    t = fk.Table(fk.Tensor(T2B128, [n, k], data))
+    m = t.matrix()
+    for rows in (1, 16):
+        xh = rng.standard_normal((rows, k)).astype(np.float32)
+        x = torch.from_numpy(xh).cuda()
+        inp = fk.QuantizedRows().input(m, x.view(-1))
+        out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+        ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 50, graph=True)
+        b = n * k // 4 + n * k // 128 * 4 + rows * (k + k // 128 * 8) + rows * n * 4
+        entry = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
+                 "bytes": b}
+        if with_cpu:
+            entry["cpu_baseline"] = cpu_product_baseline(np, T2B128, n, k, data, xh, lambda ms_: b / ms_ / 1e6, "GB/s",
+                                                         f"the whole product, {rows} f32 row(s) quantized first")
+        res[f"t2_14336x4096_rows{rows}"] = entry
     # 4. int8 attention (attention::attend) at the DiT block's shape: 4096 tokens, 16 heads of 72
     #    read by stride and offset from one fused qkv row, exp_fast
     tokens, heads, hd = 4096, 16, 72

@@ -1116,6 +1116,198 @@ __global__ __launch_bounds__(256) void t2_product_kernel(const uint8_t *__restri
     *o = accumulate ? *o + s : s;
 }
 
+// T2b128 products, streamed: R activation rows per slice of the grid's second dimension, one
+// wave per quad of 4 outputs. A quad's codes are one run of B·32 bytes (matmul.rs:461-469: per
+// block, each output's 8 bytes hold 4 two-bit parts of 8 inputs), read 1 KiB (32 blocks, 8
+// groups of 128) per load instruction with a ring of kT2Ring chunks in flight. Lane l takes
+// block 4·(l/8) + l%4 of the chunk and outputs 2·((l/4)%2) + {0, 1}, so the four blocks of a
+// group sit in one quad of lanes and their int32 dots sum by two DPP steps. Each group's term
+// goes to the wave's LDS row for its (row, output); after the last chunk lanes 0..4R-1, one per
+// (row, output), add their row in group order: s = fl(s + fl(fl((float)D_g) · fl(ws · as))),
+// or s = fma((float)D_g, ws · as, s) under the fused scaling.
+struct T2Params {
+    const uint8_t *codes;
+    const float *wscales;
+    int B, G, K, n_rows;
+    const int8_t *q;  // [rows][K] levels, 16-byte aligned rows
+    const float *as;  // [rows][G]
+    const int32_t *corr;
+    int rows;
+    int quad_begin, quad_end, col_begin;
+    const float *bias;
+    float *out;
+    long ld_out;
+    int accumulate;
+};
+
+constexpr int kT2Ring = 4;
+
+// A (row, output)'s LDS row of group terms: G floats padded to whole float4s and 4 more, so the
+// rows of neighbouring lanes start in different banks.
+__host__ __device__ inline int t2_row_stride(int G) { return (G + 3) / 4 * 4 + 4; }
+
+// Dynamic LDS of one workgroup: R rows of levels, R rows of (scale, correction), and per wave R
+// x 4 rows of group terms (two floats a group, D and ws·as, under the fused scaling).
+inline size_t t2_lds_bytes(int R, int K, int G, bool fused)
+{
+    return size_t(R) * K + size_t(R) * G * 8 + 4 * size_t(R) * 4 * t2_row_stride(G) * 4 * (fused ? 2 : 1);
+}
+
+template <int R, bool FUSED>
+__global__ __launch_bounds__(256) void t2_rows_kernel(T2Params p)
+{
+    extern __shared__ __align__(16) unsigned char t2_lds[];
+    const int G = p.G, Gp = t2_row_stride(G);
+    int4 *act = reinterpret_cast<int4 *>(t2_lds);
+    float *rs = reinterpret_cast<float *>(t2_lds + size_t(R) * p.K);
+    int *rc = reinterpret_cast<int *>(rs + R * G);
+    float *tb = reinterpret_cast<float *>(rc + R * G);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = blockIdx.y * R, nr = min(R, p.rows - row0);
+    const int quad = p.quad_begin + blockIdx.x * 4 + wave;
+    const bool live = quad < p.quad_end;
+    const int jj = lane & 3, hh = (lane >> 2) & 1, gq = lane >> 3;
+    const int blk = 4 * gq + jj;        // this lane's block in a chunk of 32
+    // its 16 bytes of the block (half hh: outputs 2·hh and 2·hh + 1) are the chunk's piece 2·blk + hh
+    const int col = 2 * hh + (jj & 1);  // the output whose term this lane writes
+    const int nchunks = (p.B + 31) >> 5;
+    const int4 *wq = reinterpret_cast<const int4 *>(p.codes + size_t(live ? quad : 0) * p.B * 32);
+    const float *wsq = p.wscales + size_t(live ? quad : 0) * G * 4;
+
+    // Every lane loads on every slot, chunks past the end included, from its block clamped into
+    // the quad's run (the same count of loads on every path keeps the waits per load exact); the
+    // terms of a block past the end are zeroed where they are formed.
+    int4 ring[kT2Ring];
+    float wsr[kT2Ring];
+    auto fetch = [&](int c, int4 &w, float &ws) {
+        const int bs = min(32 * c + blk, p.B - 1);
+        w = wq[2 * bs + hh];
+        ws = wsq[(bs >> 2) * 4 + col];
+    };
+#pragma unroll
+    for (int i = 0; i < kT2Ring; i++) fetch(i, ring[i], wsr[i]);
+
+    const int kv = p.K >> 4;
+    for (int i = threadIdx.x; i < R * kv; i += 256) {
+        const int r = i / kv, j = i - r * kv;
+        act[i] = r < nr ? reinterpret_cast<const int4 *>(p.q + size_t(row0 + r) * p.K)[j] : make_int4(0, 0, 0, 0);
+    }
+    for (int i = threadIdx.x; i < R * G; i += 256) {
+        const int r = i / G, g = i - r * G;
+        rs[i] = r < nr ? p.as[size_t(row0 + r) * G + g] : 0.0f;
+        rc[i] = r < nr ? p.corr[size_t(row0 + r) * G + g] : 0;
+    }
+    __syncthreads();
+    if (!live) return;
+
+    // this wave's term rows: [R x 4][Gp] floats (D), and under the fused scaling [R x 4][Gp] of ws·as
+    float *tw = tb + size_t(wave) * R * 4 * Gp * (FUSED ? 2 : 1);
+    auto process = [&](int c, const int4 w, const float ws) {
+        const int b = min(32 * c + blk, p.B - 1), g = min(8 * c + gq, G - 1);
+        const bool real = 8 * c + gq < G;
+        int cw[16];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            cw[4 * t + 0] = (w.x >> (2 * t)) & 0x03030303;
+            cw[4 * t + 1] = (w.y >> (2 * t)) & 0x03030303;
+            cw[4 * t + 2] = (w.z >> (2 * t)) & 0x03030303;
+            cw[4 * t + 3] = (w.w >> (2 * t)) & 0x03030303;
+        }
+        // every LDS read of the chunk first (indices clamped into range, so no read is skipped)
+        int4 a0[R], a1[R];
+        int cv[R];
+        float sv[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            a0[r] = act[((r * p.K) >> 4) + 2 * b];
+            a1[r] = act[((r * p.K) >> 4) + 2 * b + 1];
+            cv[r] = rc[r * G + g];
+            sv[r] = rs[r * G + g];
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int a[8] = {a0[r].x, a0[r].y, a0[r].z, a0[r].w, a1[r].x, a1[r].y, a1[r].z, a1[r].w};
+            int d0 = 0, d1 = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                d0 = dot4(cw[4 * t + 0], a[2 * t], d0);
+                d0 = dot4(cw[4 * t + 1], a[2 * t + 1], d0);
+                d1 = dot4(cw[4 * t + 2], a[2 * t], d1);
+                d1 = dot4(cw[4 * t + 3], a[2 * t + 1], d1);
+            }
+            d0 += xor1(d0);
+            d0 += xor2(d0);
+            d1 += xor1(d1);
+            d1 += xor2(d1);
+            const float f = real ? float(cv[r] + ((jj & 1) ? d1 : d0)) : 0.0f;
+            const float sc = real ? ws * sv[r] : 0.0f;
+            // lanes jj and jj + 2 hold the same group, output and values: both write them
+            float *row = tw + (r * 4 + col) * Gp * (FUSED ? 2 : 1);
+            if (FUSED) {
+                row[8 * c + gq] = f;
+                row[Gp + 8 * c + gq] = sc;
+            } else {
+                row[8 * c + gq] = f * sc;
+            }
+        }
+    };
+
+    for (int c0 = 0; c0 < nchunks; c0 += kT2Ring) {
+#pragma unroll
+        for (int i = 0; i < kT2Ring; i++) {
+            const int c = c0 + i;
+            const int4 w = ring[i];
+            const float ws = wsr[i];
+            fetch(c + kT2Ring, ring[i], wsr[i]);
+            if (c < nchunks) process(c, w, ws);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // the group-order sums, one (row, output) per lane; terms of groups past G are +0, which
+    // leaves every sum as it is (a sum that starts at +0 is never -0)
+    if (lane < 4 * R && (lane >> 2) < nr) {
+        const float *tl = tw + lane * Gp * (FUSED ? 2 : 1);
+        float s = 0.0f;
+        for (int g = 0; g < G; g += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(tl + g);
+            if (FUSED) {
+                const float4 u = *reinterpret_cast<const float4 *>(tl + Gp + g);
+                s = __builtin_fmaf(v.x, u.x, s);
+                s = __builtin_fmaf(v.y, u.y, s);
+                s = __builtin_fmaf(v.z, u.z, s);
+                s = __builtin_fmaf(v.w, u.w, s);
+            } else {
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+        }
+        const int n = quad * 4 + (lane & 3);
+        if (p.bias && n < p.n_rows) s = s + p.bias[n];
+        float *o = p.out + size_t(row0 + (lane >> 2)) * p.ld_out + (n - p.col_begin);
+        *o = p.accumulate ? *o + s : s;
+    }
+}
+
+template <int R, bool FUSED>
+int launch_t2_rows(const T2Params &p, size_t lds, hipStream_t s)
+{
+    const unsigned gx = unsigned((p.quad_end - p.quad_begin + 3) / 4), gy = unsigned((p.rows + R - 1) / R);
+    t2_rows_kernel<R, FUSED><<<dim3(gx, gy), 256, lds, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+template <int R>
+int launch_t2_rows(const T2Params &p, bool fused, hipStream_t s)
+{
+    const size_t lds = t2_lds_bytes(R, p.K, p.G, fused);
+    return fused ? launch_t2_rows<R, true>(p, lds, s) : launch_t2_rows<R, false>(p, lds, s);
+}
+
 }  // namespace
 
 // Workspaces come from a stream-ordered pool per device that keeps freed memory for the next
@@ -1256,7 +1448,35 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         as = sc;
         corr = co;
     }
-    if (rc == FG_OK) {
+    // the streamed kernel for outputs (the int32 dots stay on the one-thread-per-output kernel)
+    const bool fused = a.fused != 0;
+    int R = M >= 5 ? 8 : M >= 3 ? 4 : M;
+    while (R > 1 && t2_lds_bytes(R, K, G, fused) > 64 * 1024) R /= 2;
+    if (rc == FG_OK && !a.dots && M > 0 && t2_lds_bytes(R, K, G, fused) <= 64 * 1024 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
+        (M + R - 1) / R <= 65535) {
+        T2Params p{};
+        p.codes = reinterpret_cast<const uint8_t *>(t->codes);
+        p.wscales = t->scales;
+        p.B = int(t->blocks);
+        p.G = G;
+        p.K = K;
+        p.n_rows = int(t->rows);
+        p.q = q;
+        p.as = as;
+        p.corr = corr;
+        p.rows = M;
+        p.quad_begin = int(a.quad_begin);
+        p.quad_end = int(a.quad_end);
+        p.col_begin = col_begin;
+        p.bias = a.bias;
+        p.out = a.out;
+        p.ld_out = long(a.ld_out);
+        p.accumulate = a.accumulate;
+        rc = R == 8   ? launch_t2_rows<8>(p, fused, s)
+             : R == 4 ? launch_t2_rows<4>(p, fused, s)
+             : R == 2 ? launch_t2_rows<2>(p, fused, s)
+                      : launch_t2_rows<1>(p, fused, s);
+    } else if (rc == FG_OK) {
         const long n = long(M) * ncols;
         t2_product_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint8_t *>(t->codes), t->scales, int(t->blocks),
                                                                    G, K, int(t->rows), q, as, corr, M, col_begin, ncols, a.bias,

@@ -393,6 +393,46 @@ def test_int4_shape_bit_exact(fk, rows):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9])
+@pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128), (5, 16384)])
+def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
+    """The streamed T2b128 kernel: 3 groups (one partial 1 KiB chunk), 9 groups (a second chunk of
+    one group), 40 groups (five chunks: the four-chunk ring refilled), one group, and 128 groups
+    (16384 levels a row: two rows per slice, not four, to fit the workgroup's LDS); 1-9 rows in
+    slices of 1, 2 or 4; 70 outputs (a last workgroup of two quads); bias and the fused scaling."""
+    print(f"t2 {rows} x {cols} -> {n_rows}", flush=True)
+    dtype = O.T2B128
+    data = synthetic_table(dtype, n_rows, cols, seed=n_rows + cols + rows)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=cols + 3 * rows, outliers=0.02)
+    bias = np.random.default_rng(rows).standard_normal(n_rows).astype(np.float32)
+    want = oracle_product(dtype, n_rows, cols, data, x, rows, bias=bias)
+    got = gpu_product(fk, t, x, rows, bias=bias)
+    assert same_bits(got, want), first_mismatch(got, want)
+    got_pre = gpu_product(fk, t, x, rows, bias=bias, fused=False)
+    assert same_bits(got_pre, want), first_mismatch(got_pre, want)
+    want_f = oracle_product(dtype, n_rows, cols, data, x, rows, fused=True)
+    got_f = gpu_product(fk, t, x, rows, fused_scale=True)
+    assert same_bits(got_f, want_f), first_mismatch(got_f, want_f)
+    lo, hi = 4 * (n_rows // 12), 4 * ((n_rows + 3) // 4)
+    want_r = oracle_product(dtype, n_rows, cols, data, x, rows, lo, hi)
+    got_r = gpu_product(fk, t, x, rows, cols=range(lo, hi))
+    assert same_bits(got_r, want_r), first_mismatch(got_r, want_r)
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_t2_large_shape_bit_exact(fk, rows):
+    """14336 x 4096 T2b128, every output against the oracle's threaded product."""
+    n, k = 14336, 4096
+    data = synthetic_table(O.T2B128, n, k, seed=2)
+    t = table(fk, O.T2B128, n, k, data)
+    x = activations(rows, k, seed=22)
+    got = gpu_product(fk, t, x, rows)
+    q, s, c = O.quantize_rows(x.reshape(-1), O.T2B128)
+    want = O.matmul_threaded(O.T2B128, n, k, data, q, s, c, rows, threads=16)
+    assert same_bits(got, want), first_mismatch(got, want)
+
+
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
 @pytest.mark.parametrize("rows,k", [(5, 32 * 8), (16, 32 * 8), (9, 32 * 17), (12, 32 * 28), (7, 32 * 3)])
 def test_small_batch_streamed_with_one_or_two_stages(fk, dtype, rows, k):

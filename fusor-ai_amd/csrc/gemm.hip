@@ -1185,18 +1185,56 @@ __global__ __launch_bounds__(256) void t2_rows_kernel(T2Params p)
         w = wq[2 * bs + hh];
         ws = wsq[(bs >> 2) * 4 + col];
     };
+
+    // The rows' levels, scales and corrections are loaded before the codes and stored to LDS
+    // after them: loads complete in order, so the stores wait for these loads only, while the
+    // codes stay in flight. The first R int4s and one (scale, correction) pair per thread go this
+    // way (R rows of up to 4096 levels, up to 256 groups), from clamped addresses (rows past the
+    // slice are zeroed at the store); larger slices finish with plain loops.
+    constexpr int kStage16 = R, kStageG = 1;
+    const int kv = p.K >> 4, n16 = R * kv, ng = R * G;
+    const int4 *q4 = reinterpret_cast<const int4 *>(p.q);
+    int4 st[kStage16];
+    float sts[kStageG];
+    int stc[kStageG];
+#pragma unroll
+    for (int k = 0; k < kStage16; k++) {
+        const int i = min(int(threadIdx.x) + 256 * k, n16 - 1), r = i / kv;
+        st[k] = q4[size_t(row0 + min(r, nr - 1)) * kv + (i - r * kv)];
+    }
+#pragma unroll
+    for (int k = 0; k < kStageG; k++) {
+        const int i = min(int(threadIdx.x) + 256 * k, ng - 1), r = i / G;
+        const size_t at = size_t(row0 + min(r, nr - 1)) * G + (i - r * G);
+        sts[k] = p.as[at];
+        stc[k] = p.corr[at];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the staging loads go out first
 #pragma unroll
     for (int i = 0; i < kT2Ring; i++) fetch(i, ring[i], wsr[i]);
-
-    const int kv = p.K >> 4;
-    for (int i = threadIdx.x; i < R * kv; i += 256) {
-        const int r = i / kv, j = i - r * kv;
-        act[i] = r < nr ? reinterpret_cast<const int4 *>(p.q + size_t(row0 + r) * p.K)[j] : make_int4(0, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // then the codes, then the stores
+#pragma unroll
+    for (int k = 0; k < kStage16; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < n16) act[i] = i / kv < nr ? st[k] : make_int4(0, 0, 0, 0);
     }
-    for (int i = threadIdx.x; i < R * G; i += 256) {
-        const int r = i / G, g = i - r * G;
-        rs[i] = r < nr ? p.as[size_t(row0 + r) * G + g] : 0.0f;
-        rc[i] = r < nr ? p.corr[size_t(row0 + r) * G + g] : 0;
+#pragma unroll
+    for (int k = 0; k < kStageG; k++) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < ng) {
+            const bool in = i / G < nr;
+            rs[i] = in ? sts[k] : 0.0f;
+            rc[i] = in ? stc[k] : 0;
+        }
+    }
+    for (int i = threadIdx.x + 256 * kStage16; i < n16; i += 256) {
+        const int r = i / kv;
+        act[i] = r < nr ? q4[size_t(row0 + r) * kv + (i - r * kv)] : make_int4(0, 0, 0, 0);
+    }
+    for (int i = threadIdx.x + 256 * kStageG; i < ng; i += 256) {
+        const int r = i / G;
+        rs[i] = r < nr ? p.as[size_t(row0 + r) * G + (i - r * G)] : 0.0f;
+        rc[i] = r < nr ? p.corr[size_t(row0 + r) * G + (i - r * G)] : 0;
     }
     __syncthreads();
     if (!live) return;
@@ -1253,14 +1291,20 @@ __global__ __launch_bounds__(256) void t2_rows_kernel(T2Params p)
         }
     };
 
-    for (int c0 = 0; c0 < nchunks; c0 += kT2Ring) {
+    if (nchunks <= kT2Ring) {  // the whole run is in flight already: no refills, no loop
 #pragma unroll
-        for (int i = 0; i < kT2Ring; i++) {
-            const int c = c0 + i;
-            const int4 w = ring[i];
-            const float ws = wsr[i];
-            fetch(c + kT2Ring, ring[i], wsr[i]);
-            if (c < nchunks) process(c, w, ws);
+        for (int i = 0; i < kT2Ring; i++)
+            if (i < nchunks) process(i, ring[i], wsr[i]);
+    } else {
+        for (int c0 = 0; c0 < nchunks; c0 += kT2Ring) {
+#pragma unroll
+            for (int i = 0; i < kT2Ring; i++) {
+                const int c = c0 + i;
+                const int4 w = ring[i];
+                const float ws = wsr[i];
+                fetch(c + kT2Ring, ring[i], wsr[i]);
+                if (c < nchunks) process(c, w, ws);
+            }
         }
     }
     __builtin_amdgcn_wave_barrier();

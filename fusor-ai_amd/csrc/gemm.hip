@@ -1336,6 +1336,146 @@ __global__ __launch_bounds__(256) void t2_rows_kernel(T2Params p)
     }
 }
 
+// T2b128 products of many rows on the int8 matrix cores: one wave per 32 x 32 output tile. Per
+// group of 128 inputs, four v_mfma_i32_32x32x32_i8 (one per block of 32) chain the group's int32
+// dots of a column's codes (0, 1, 2 as they are) with the rows' levels; the group total adds
+// the row's correction (matmul.rs:461-469 with the quantizer's Backend::seed), and the exact
+// rescale follows once per group: s = fl(s + fl(fl((float)D_g) · fl(ws · as))), or one fma
+// under the fused scaling. Lane l feeds row (or column) l % 32 and the block's inputs
+// 16·(l/32) .. + 15: from the column's 8 bytes (lo: inputs 8t + 0..3 at bits 2t, hi: 8t + 4..7),
+// parts 2·(l/32) and 2·(l/32) + 1. Result: lane l holds column l % 32, rows 8·(v/4) + 4·(l/32)
+// + v%4. The tile's scales and corrections sit in LDS ([G][32] each); operands stream two groups
+// ahead in registers, rows and columns past the edges re-reading the last valid one.
+constexpr int kT2GemmDepth = 2;  // groups in flight
+// rows from which the matrix cores take a T2b128 product: up to 8 rows are one slice of the
+// streamed kernel (14336 x 4096: 14 µs at 8 rows), 9-16 would be two (28 µs) against one row of
+// 32 x 32 tiles here (18 µs)
+constexpr int kT2GemmRows = 9;
+
+struct T2Stage {
+    v4i a[4];    // this lane's 16 levels of each of the group's blocks
+    int2 w[4];   // its column's 8 code bytes of each block
+    float ws;    // the column's scale for the group
+};
+
+template <bool FUSED>
+__global__ __launch_bounds__(64) void t2_gemm_kernel(T2Params p)
+{
+    extern __shared__ __align__(16) float t2_tile[];  // [G][32] scales, then [G][32] corrections
+    const int G = p.G, K = p.K;
+    float *tsc = t2_tile;
+    int *tco = reinterpret_cast<int *>(t2_tile + G * 32);
+    const int lane = threadIdx.x, i = lane & 31, h = lane >> 5;
+    const int ncol = (p.quad_end - p.quad_begin) * 4, col_begin = p.quad_begin * 4;
+    int tx, ty;
+    tile_of(int(blockIdx.x), (ncol + 31) / 32, (p.rows + 31) / 32, tx, ty);
+    const int m0 = ty * 32, n0 = col_begin + tx * 32;
+    const int row = min(m0 + i, p.rows - 1);
+    const int nc = min(n0 + i, col_begin + ncol - 1);
+    const int8_t *arow = p.q + size_t(row) * K + h * 16;
+    const uint8_t *wcol = p.codes + size_t(nc >> 2) * p.B * 32 + (nc & 3) * 8;
+    const float *wscol = p.wscales + size_t(nc >> 2) * G * 4 + (nc & 3);
+
+    // rows m0 .. m0 + 31's scales and corrections, transposed to [group][row]: lane l takes row
+    // l % 32 and the groups of parity l / 32, eight loads (clamped) before their stores
+    for (int g0 = h; g0 < G; g0 += 16) {
+        float a8[8];
+        int c8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t at = size_t(row) * G + min(g0 + 2 * u, G - 1);
+            a8[u] = p.as[at];
+            c8[u] = p.corr[at];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int g = g0 + 2 * u;
+            if (g < G) {
+                tsc[g * 32 + i] = a8[u];
+                tco[g * 32 + i] = c8[u];
+            }
+        }
+    }
+    __syncthreads();
+
+    auto fetch = [&](int g, T2Stage &st) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            st.a[k] = *reinterpret_cast<const v4i *>(arow + (4 * g + k) * 32);
+            st.w[k] = *reinterpret_cast<const int2 *>(wcol + size_t(4 * g + k) * 32);
+        }
+        st.ws = wscol[size_t(g) * 4];
+    };
+    auto product = [&](const T2Stage &st) {
+        v16i d = {0};
+        const int sh = 4 * h;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int lo = st.w[k].x, hi = st.w[k].y;
+            const v4i w = {(lo >> sh) & 0x03030303, (hi >> sh) & 0x03030303, (lo >> (sh + 2)) & 0x03030303,
+                           (hi >> (sh + 2)) & 0x03030303};
+            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(st.a[k], w, d, 0, 0, 0);
+        }
+        return d;
+    };
+    float acc[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+    auto rescale = [&](int g, const T2Stage &st, const v16i d) {
+        const v4f *ls = reinterpret_cast<const v4f *>(tsc + g * 32 + 4 * h);
+        const v4i *lc = reinterpret_cast<const v4i *>(tco + g * 32 + 4 * h);
+        const v4f s0 = ls[0], s1 = ls[2], s2 = ls[4], s3 = ls[6];
+        const v4i c0 = lc[0], c1 = lc[2], c2 = lc[4], c3 = lc[6];
+        const float sc[16] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w, s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
+        const int co[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float D = float(co[v] + d[v]);
+            acc[v] = FUSED ? __builtin_fmaf(D, st.ws * sc[v], acc[v]) : acc[v] + D * (st.ws * sc[v]);
+        }
+    };
+
+    // group g lives in stage g % kT2GemmDepth; its refill (clamped at the last group, so no
+    // branch splits the loads) follows its rescale
+    T2Stage st[kT2GemmDepth];
+#pragma unroll
+    for (int k = 0; k < kT2GemmDepth; k++) {
+        fetch(min(k, G - 1), st[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int g = 0; g < G; g += kT2GemmDepth) {
+#pragma unroll
+        for (int k = 0; k < kT2GemmDepth; k++) {
+            if (g + k < G) {
+                const v16i d = product(st[k]);
+                rescale(g + k, st[k], d);
+            }
+            fetch(min(g + k + kT2GemmDepth, G - 1), st[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const int n = n0 + i;
+    if (n >= col_begin + ncol) return;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (r >= p.rows) continue;
+        float y = acc[v];
+        if (p.bias && n < p.n_rows) y = y + p.bias[n];
+        float *o = p.out + size_t(r) * p.ld_out + (n - col_begin);
+        *o = p.accumulate ? *o + y : y;
+    }
+}
+
+template <bool FUSED>
+int launch_t2_gemm(const T2Params &p, hipStream_t s)
+{
+    const long tiles = long((p.quad_end - p.quad_begin) * 4 + 31) / 32 * ((p.rows + 31) / 32);
+    t2_gemm_kernel<FUSED><<<unsigned(tiles), 64, size_t(p.G) * 32 * 8, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
 template <int R, bool FUSED>
 int launch_t2_rows(const T2Params &p, size_t lds, hipStream_t s)
 {
@@ -1492,8 +1632,35 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         as = sc;
         corr = co;
     }
-    // the streamed kernel for outputs (the int32 dots stay on the one-thread-per-output kernel)
+    // the matrix cores for many rows, the streamed kernel for few (the int32 dots stay on the
+    // one-thread-per-output kernel)
     const bool fused = a.fused != 0;
+    if (rc == FG_OK && !a.dots && M >= kT2GemmRows && size_t(G) * 32 * 8 <= 64 * 1024 && (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
+        T2Params p{};
+        p.codes = reinterpret_cast<const uint8_t *>(t->codes);
+        p.wscales = t->scales;
+        p.B = int(t->blocks);
+        p.G = G;
+        p.K = K;
+        p.n_rows = int(t->rows);
+        p.q = q;
+        p.as = as;
+        p.corr = corr;
+        p.rows = M;
+        p.quad_begin = int(a.quad_begin);
+        p.quad_end = int(a.quad_end);
+        p.col_begin = col_begin;
+        p.bias = a.bias;
+        p.out = a.out;
+        p.ld_out = long(a.ld_out);
+        p.accumulate = a.accumulate;
+        rc = fused ? launch_t2_gemm<true>(p, s) : launch_t2_gemm<false>(p, s);
+        if (owned) {
+            hipError_t e = hipFreeAsync(ws, s);
+            if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");
+        }
+        return rc;
+    }
     int R = M >= 5 ? 8 : M >= 3 ? 4 : M;
     while (R > 1 && t2_lds_bytes(R, K, G, fused) > 64 * 1024) R /= 2;
     if (rc == FG_OK && !a.dots && M > 0 && t2_lds_bytes(R, K, G, fused) <= 64 * 1024 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&

@@ -393,13 +393,14 @@ def test_int4_shape_bit_exact(fk, rows):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 9])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128), (5, 16384)])
 def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
-    """The streamed T2b128 kernel: 3 groups (one partial 1 KiB chunk), 9 groups (a second chunk of
-    one group), 40 groups (five chunks: the four-chunk ring refilled), one group, and 128 groups
-    (16384 levels a row: two rows per slice, not four, to fit the workgroup's LDS); 1-9 rows in
-    slices of 1, 2 or 4; 70 outputs (a last workgroup of two quads); bias and the fused scaling."""
+    """The streamed T2b128 kernel (up to 8 rows): 3 groups (one partial 1 KiB chunk), 9 groups (a
+    second chunk of one group), 40 groups (five chunks: the four-chunk ring refilled), one group,
+    and 128 groups (16384 levels a row: slices of two rows, not four or eight, to fit the
+    workgroup's LDS); slices of 1, 2, 4 or 8 rows; 70 outputs (a last workgroup of two quads);
+    bias and the fused scaling."""
     print(f"t2 {rows} x {cols} -> {n_rows}", flush=True)
     dtype = O.T2B128
     data = synthetic_table(dtype, n_rows, cols, seed=n_rows + cols + rows)
@@ -418,6 +419,46 @@ def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
     want_r = oracle_product(dtype, n_rows, cols, data, x, rows, lo, hi)
     got_r = gpu_product(fk, t, x, rows, cols=range(lo, hi))
     assert same_bits(got_r, want_r), first_mismatch(got_r, want_r)
+
+
+@pytest.mark.parametrize("rows", [9, 16, 31, 33, 100])
+@pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128)])
+def test_t2_on_the_matrix_cores(fk, rows, n_rows, cols):
+    """T2b128 products of 9 or more rows (the int8 matrix cores, a group's four blocks chained in
+    one accumulator): 3, 9, 40 and 1 groups (odd counts against the two-group ring), partial row
+    tiles (9, 31, 33, 100 rows) and column tiles (70 outputs), bias, the fused scaling, a column
+    range, pre-quantized rows."""
+    print(f"t2 mfma {rows} x {cols} -> {n_rows}", flush=True)
+    dtype = O.T2B128
+    data = synthetic_table(dtype, n_rows, cols, seed=n_rows + cols + rows + 1)
+    t = table(fk, dtype, n_rows, cols, data)
+    x = activations(rows, cols, seed=cols + 5 * rows, outliers=0.02)
+    bias = np.random.default_rng(rows + 1).standard_normal(n_rows).astype(np.float32)
+    want = oracle_product(dtype, n_rows, cols, data, x, rows, bias=bias)
+    got = gpu_product(fk, t, x, rows, bias=bias)
+    assert same_bits(got, want), first_mismatch(got, want)
+    got_pre = gpu_product(fk, t, x, rows, bias=bias, fused=False)
+    assert same_bits(got_pre, want), first_mismatch(got_pre, want)
+    want_f = oracle_product(dtype, n_rows, cols, data, x, rows, fused=True)
+    got_f = gpu_product(fk, t, x, rows, fused_scale=True)
+    assert same_bits(got_f, want_f), first_mismatch(got_f, want_f)
+    lo, hi = 4 * (n_rows // 12), 4 * ((n_rows + 3) // 4)
+    want_r = oracle_product(dtype, n_rows, cols, data, x, rows, lo, hi)
+    got_r = gpu_product(fk, t, x, rows, cols=range(lo, hi))
+    assert same_bits(got_r, want_r), first_mismatch(got_r, want_r)
+
+
+def test_t2_many_tiles_bit_exact(fk):
+    """128 rows x 4096 -> 2048 T2b128 (256 tiles in the per-XCD order), every output against the
+    oracle's threaded product."""
+    rows, n, k = 128, 2048, 4096
+    data = synthetic_table(O.T2B128, n, k, seed=12)
+    t = table(fk, O.T2B128, n, k, data)
+    x = activations(rows, k, seed=13, outliers=0.01)
+    got = gpu_product(fk, t, x, rows)
+    q, s, c = O.quantize_rows(x.reshape(-1), O.T2B128)
+    want = O.matmul_threaded(O.T2B128, n, k, data, q, s, c, rows, threads=16)
+    assert same_bits(got, want), first_mismatch(got, want)
 
 
 @pytest.mark.parametrize("rows", [1, 16])

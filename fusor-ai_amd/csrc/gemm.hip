@@ -1351,14 +1351,21 @@ constexpr int kT2GemmDepth = 2;  // groups in flight
 // streamed kernel (14336 x 4096: 14 µs at 8 rows), 9-16 would be two (28 µs) against one row of
 // 32 x 32 tiles here (18 µs)
 constexpr int kT2GemmRows = 9;
+#ifndef FG_T2_WIDE_TILES
+#define FG_T2_WIDE_TILES 2048
+#endif
+constexpr long kT2WideTiles = FG_T2_WIDE_TILES;
 
+template <int TN>
 struct T2Stage {
-    v4i a[4];    // this lane's 16 levels of each of the group's blocks
-    int2 w[4];   // its column's 8 code bytes of each block
-    float ws;    // the column's scale for the group
+    v4i a[4];       // this lane's 16 levels of each of the group's blocks
+    int2 w[TN][4];  // its column's 8 code bytes of each block, per 32-column sub-tile
+    float ws[TN];   // the column's scale for the group
 };
 
-template <bool FUSED>
+// TN: 32-column sub-tiles per wave (TN MFMA chains share the rows' operands, halving their
+// reads at TN = 2).
+template <int TN, bool FUSED>
 __global__ __launch_bounds__(64) void t2_gemm_kernel(T2Params p)
 {
     extern __shared__ __align__(16) float t2_tile[];  // [G][32] scales, then [G][32] corrections
@@ -1368,13 +1375,18 @@ __global__ __launch_bounds__(64) void t2_gemm_kernel(T2Params p)
     const int lane = threadIdx.x, i = lane & 31, h = lane >> 5;
     const int ncol = (p.quad_end - p.quad_begin) * 4, col_begin = p.quad_begin * 4;
     int tx, ty;
-    tile_of(int(blockIdx.x), (ncol + 31) / 32, (p.rows + 31) / 32, tx, ty);
-    const int m0 = ty * 32, n0 = col_begin + tx * 32;
+    tile_of(int(blockIdx.x), (ncol + 32 * TN - 1) / (32 * TN), (p.rows + 31) / 32, tx, ty);
+    const int m0 = ty * 32, n0 = col_begin + tx * 32 * TN;
     const int row = min(m0 + i, p.rows - 1);
-    const int nc = min(n0 + i, col_begin + ncol - 1);
     const int8_t *arow = p.q + size_t(row) * K + h * 16;
-    const uint8_t *wcol = p.codes + size_t(nc >> 2) * p.B * 32 + (nc & 3) * 8;
-    const float *wscol = p.wscales + size_t(nc >> 2) * G * 4 + (nc & 3);
+    const uint8_t *wcol[TN];
+    const float *wscol[TN];
+#pragma unroll
+    for (int t = 0; t < TN; t++) {
+        const int nc = min(n0 + 32 * t + i, col_begin + ncol - 1);
+        wcol[t] = p.codes + size_t(nc >> 2) * p.B * 32 + (nc & 3) * 8;
+        wscol[t] = p.wscales + size_t(nc >> 2) * G * 4 + (nc & 3);
+    }
 
     // rows m0 .. m0 + 31's scales and corrections, transposed to [group][row]: lane l takes row
     // l % 32 and the groups of parity l / 32, eight loads (clamped) before their stores
@@ -1398,30 +1410,34 @@ __global__ __launch_bounds__(64) void t2_gemm_kernel(T2Params p)
     }
     __syncthreads();
 
-    auto fetch = [&](int g, T2Stage &st) {
+    auto fetch = [&](int g, T2Stage<TN> &st) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             st.a[k] = *reinterpret_cast<const v4i *>(arow + (4 * g + k) * 32);
-            st.w[k] = *reinterpret_cast<const int2 *>(wcol + size_t(4 * g + k) * 32);
+#pragma unroll
+            for (int t = 0; t < TN; t++) st.w[t][k] = *reinterpret_cast<const int2 *>(wcol[t] + size_t(4 * g + k) * 32);
         }
-        st.ws = wscol[size_t(g) * 4];
+#pragma unroll
+        for (int t = 0; t < TN; t++) st.ws[t] = wscol[t][size_t(g) * 4];
     };
-    auto product = [&](const T2Stage &st) {
+    auto product = [&](const T2Stage<TN> &st, int t) {
         v16i d = {0};
         const int sh = 4 * h;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int lo = st.w[k].x, hi = st.w[k].y;
+            const int lo = st.w[t][k].x, hi = st.w[t][k].y;
             const v4i w = {(lo >> sh) & 0x03030303, (hi >> sh) & 0x03030303, (lo >> (sh + 2)) & 0x03030303,
                            (hi >> (sh + 2)) & 0x03030303};
             d = __builtin_amdgcn_mfma_i32_32x32x32_i8(st.a[k], w, d, 0, 0, 0);
         }
         return d;
     };
-    float acc[16];
+    float acc[TN][16];
 #pragma unroll
-    for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-    auto rescale = [&](int g, const T2Stage &st, const v16i d) {
+    for (int t = 0; t < TN; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+    auto rescale = [&](int g, const T2Stage<TN> &st, int t, const v16i d) {
         const v4f *ls = reinterpret_cast<const v4f *>(tsc + g * 32 + 4 * h);
         const v4i *lc = reinterpret_cast<const v4i *>(tco + g * 32 + 4 * h);
         const v4f s0 = ls[0], s1 = ls[2], s2 = ls[4], s3 = ls[6];
@@ -1431,13 +1447,13 @@ __global__ __launch_bounds__(64) void t2_gemm_kernel(T2Params p)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             const float D = float(co[v] + d[v]);
-            acc[v] = FUSED ? __builtin_fmaf(D, st.ws * sc[v], acc[v]) : acc[v] + D * (st.ws * sc[v]);
+            acc[t][v] = FUSED ? __builtin_fmaf(D, st.ws[t] * sc[v], acc[t][v]) : acc[t][v] + D * (st.ws[t] * sc[v]);
         }
     };
 
     // group g lives in stage g % kT2GemmDepth; its refill (clamped at the last group, so no
     // branch splits the loads) follows its rescale
-    T2Stage st[kT2GemmDepth];
+    T2Stage<TN> st[kT2GemmDepth];
 #pragma unroll
     for (int k = 0; k < kT2GemmDepth; k++) {
         fetch(min(k, G - 1), st[k]);
@@ -1447,33 +1463,44 @@ __global__ __launch_bounds__(64) void t2_gemm_kernel(T2Params p)
 #pragma unroll
         for (int k = 0; k < kT2GemmDepth; k++) {
             if (g + k < G) {
-                const v16i d = product(st[k]);
-                rescale(g + k, st[k], d);
+#pragma unroll
+                for (int t = 0; t < TN; t++) rescale(g + k, st[k], t, product(st[k], t));
             }
             fetch(min(g + k + kT2GemmDepth, G - 1), st[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    const int n = n0 + i;
-    if (n >= col_begin + ncol) return;
 #pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (r >= p.rows) continue;
-        float y = acc[v];
-        if (p.bias && n < p.n_rows) y = y + p.bias[n];
-        float *o = p.out + size_t(r) * p.ld_out + (n - col_begin);
-        *o = p.accumulate ? *o + y : y;
+    for (int t = 0; t < TN; t++) {
+        const int n = n0 + 32 * t + i;
+        if (n >= col_begin + ncol) continue;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int r = m0 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (r >= p.rows) continue;
+            float y = acc[t][v];
+            if (p.bias && n < p.n_rows) y = y + p.bias[n];
+            float *o = p.out + size_t(r) * p.ld_out + (n - col_begin);
+            *o = p.accumulate ? *o + y : y;
+        }
     }
 }
 
+template <int TN, bool FUSED>
+int launch_t2_gemm_as(const T2Params &p, hipStream_t s)
+{
+    const long tiles = long((p.quad_end - p.quad_begin) * 4 + 32 * TN - 1) / (32 * TN) * ((p.rows + 31) / 32);
+    t2_gemm_kernel<TN, FUSED><<<unsigned(tiles), 64, size_t(p.G) * 32 * 8, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
+// 32 x 64 tiles while they still give every SIMD two waves, else 32 x 32
 template <bool FUSED>
 int launch_t2_gemm(const T2Params &p, hipStream_t s)
 {
-    const long tiles = long((p.quad_end - p.quad_begin) * 4 + 31) / 32 * ((p.rows + 31) / 32);
-    t2_gemm_kernel<FUSED><<<unsigned(tiles), 64, size_t(p.G) * 32 * 8, s>>>(p);
-    FG_HIP(hipGetLastError());
-    return FG_OK;
+    const long wide = long((p.quad_end - p.quad_begin) * 4 + 63) / 64 * ((p.rows + 31) / 32);
+    return wide >= kT2WideTiles ? launch_t2_gemm_as<2, FUSED>(p, s) : launch_t2_gemm_as<1, FUSED>(p, s);
 }
 
 template <int R, bool FUSED>

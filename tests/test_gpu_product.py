@@ -461,6 +461,22 @@ def test_t2_many_tiles_bit_exact(fk):
     assert same_bits(got, want), first_mismatch(got, want)
 
 
+def test_t2_wide_tiles_bit_exact(fk):
+    """512 rows x 128 -> 8196 T2b128: 2064 tiles of 32 x 64 (two MFMA chains per wave sharing the
+    rows' operands), the last holding 4 columns; every output, with the fused scaling too."""
+    rows, n, k = 512, 8196, 128
+    data = synthetic_table(O.T2B128, n, k, seed=14)
+    t = table(fk, O.T2B128, n, k, data)
+    x = activations(rows, k, seed=15, outliers=0.01)
+    q, s, c = O.quantize_rows(x.reshape(-1), O.T2B128)
+    got = gpu_product(fk, t, x, rows)
+    want = O.matmul_threaded(O.T2B128, n, k, data, q, s, c, rows, threads=16)
+    assert same_bits(got, want), first_mismatch(got, want)
+    got_f = gpu_product(fk, t, x, rows, fused_scale=True)
+    want_f = oracle_product(O.T2B128, n, k, data, x, rows, fused=True)
+    assert same_bits(got_f, want_f), first_mismatch(got_f, want_f)
+
+
 @pytest.mark.parametrize("rows", [1, 16])
 def test_t2_large_shape_bit_exact(fk, rows):
     """14336 x 4096 T2b128, every output against the oracle's threaded product."""

@@ -517,6 +517,21 @@ def extras(fk, torch, np, with_cpu=True):
             entry["cpu_baseline"] = cpu_product_baseline(np, T2B128, n, k, data, xh, lambda ms_: b / ms_ / 1e6, "GB/s",
                                                          f"the whole product, {rows} f32 row(s) quantized first")
         res[f"t2_14336x4096_rows{rows}"] = entry
+    # 3c. the same T2b128 table times 512 rows (prefill-sized: the matrix cores)
+    rows, cpu_rows = 512, 16
+    xh = rng.standard_normal((rows, k)).astype(np.float32)
+    x = torch.from_numpy(xh).cuda()
+    inp = fk.QuantizedRows().input(m, x.view(-1))
+    out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 20, graph=True)
+    ops = 2.0 * rows * n * k
+    entry = {"us": round(ms * 1e3, 2), "TOPS": round(ops / ms / 1e9, 1), "frac_int8_peak": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)}
+    if with_cpu:
+        cpu_ops = 2.0 * cpu_rows * n * k
+        entry["cpu_baseline"] = cpu_product_baseline(
+            np, T2B128, n, k, data, xh[:cpu_rows], lambda ms_: cpu_ops / ms_ / 1e9, "TOPS",
+            f"the first {cpu_rows} of {rows} rows (rows are independent), f32 rows quantized first")
+    res["t2_512x4096x14336"] = entry
     # 4. int8 attention (attention::attend) at the DiT block's shape: 4096 tokens, 16 heads of 72
     #    read by stride and offset from one fused qkv row, exp_fast
     tokens, heads, hd = 4096, 16, 72

@@ -1347,10 +1347,10 @@ __global__ __launch_bounds__(256) void t2_rows_kernel(T2Params p)
 // + v%4. The tile's scales and corrections sit in LDS ([G][32] each); operands stream two groups
 // ahead in registers, rows and columns past the edges re-reading the last valid one.
 constexpr int kT2GemmDepth = 2;  // groups in flight
-// rows from which the matrix cores take a T2b128 product: up to 8 rows are one slice of the
-// streamed kernel (14336 x 4096: 14 µs at 8 rows), 9-16 would be two (28 µs) against one row of
-// 32 x 32 tiles here (18 µs)
-constexpr int kT2GemmRows = 9;
+// rows from which the 32 x 32 tiles take a T2b128 product; 5 to 16 rows go to the 16 x 16 tiles
+// below (14336 x 4096: 11.4 µs at 9 rows, 15.1 at 16, against 17.6 for one row of 32 x 32 tiles
+// and 17.1 for the streamed kernel's 8-row slice)
+constexpr int kT2GemmRows = 17;
 #ifndef FG_T2_WIDE_TILES
 #define FG_T2_WIDE_TILES 2048
 #endif
@@ -1501,6 +1501,135 @@ int launch_t2_gemm(const T2Params &p, hipStream_t s)
 {
     const long wide = long((p.quad_end - p.quad_begin) * 4 + 63) / 64 * ((p.rows + 31) / 32);
     return wide >= kT2WideTiles ? launch_t2_gemm_as<2, FUSED>(p, s) : launch_t2_gemm_as<1, FUSED>(p, s);
+}
+
+// T2b128 products of 5 to 16 rows on the int8 matrix cores: one wave per 16 x 16 output tile, so
+// 14336 outputs take 896 waves where 32 x 32 tiles give 448 with half their rows repeated. Per
+// group of 128 inputs, four v_mfma_i32_16x16x32_i8 chain the group's int32 dots; the correction
+// and the exact rescale follow as in the 32 x 32 kernel above. An integer dot does not depend on
+// which step takes which input as long as both operands agree, so each lane reads its row's group
+// in two 16-byte pieces, inputs 16·(l/16) + 0..15 and 64 + 16·(l/16) + 0..15 (a row's 128 bytes in
+// two loads of 64 bytes per row), and step j takes 8 bytes of piece j/2: inputs
+// 64·(j/2) + 16·(l/16) + 8·(j%2) + 0..7, which lie in block 2·(j/2) + (l/16)/2 at offset
+// 16·((l/16)%2) + 8·(j%2): from that block's 8 code bytes, bits 2t, t = 2·((l/16)%2) + j%2, of
+// every byte of the lo word (inputs + 0..3) and of the hi word (+ 4..7). Lane l feeds row (or
+// column) l % 16. Result: lane l holds column l % 16, rows 4·(l/16) + v, v = 0..3. The tile's
+// scales and corrections sit in LDS ([G][16] each); operands stream four groups ahead in registers.
+constexpr int kT2Gemm16Depth = 4;  // groups in flight
+#ifndef FG_T2_MFMA16_ROWS
+#define FG_T2_MFMA16_ROWS 5
+#endif
+constexpr int kT2Gemm16Rows = FG_T2_MFMA16_ROWS;  // fewest rows taken by the 16 x 16 kernel
+
+typedef long v2l __attribute__((ext_vector_type(2)));
+struct T2Stage16 {
+    v2l a[2];    // this lane's two 16-byte pieces of its row's group
+    int2 w[2];   // its column's 8 code bytes of blocks (l/16)/2 and 2 + (l/16)/2
+    float ws;    // the column's scale for the group
+};
+
+template <bool FUSED>
+__global__ __launch_bounds__(64) void t2_gemm16_kernel(T2Params p)
+{
+    extern __shared__ __align__(16) float t2_tile16[];  // [G][16] scales, then [G][16] corrections
+    const int G = p.G, K = p.K;
+    float *tsc = t2_tile16;
+    int *tco = reinterpret_cast<int *>(t2_tile16 + G * 16);
+    const int lane = threadIdx.x, i = lane & 15, s = lane >> 4;
+    const int ncol = (p.quad_end - p.quad_begin) * 4, col_begin = p.quad_begin * 4;
+    int tx, ty;
+    tile_of(int(blockIdx.x), (ncol + 15) / 16, (p.rows + 15) / 16, tx, ty);
+    const int m0 = ty * 16, n0 = col_begin + tx * 16;
+    const int row = min(m0 + i, p.rows - 1);  // rows and columns past the edges re-read the last valid one
+    const int8_t *arow = p.q + size_t(row) * K + s * 16;
+    const int nc = min(n0 + i, col_begin + ncol - 1);
+    const uint8_t *wcol = p.codes + size_t(nc >> 2) * p.B * 32 + (nc & 3) * 8;
+    const float *wscol = p.wscales + size_t(nc >> 2) * G * 4 + (nc & 3);
+
+    // rows m0 .. m0 + 15's scales and corrections, transposed to [group][row]: lane l takes row
+    // l % 16 and the groups congruent to l / 16 mod 4, eight loads (clamped) before their stores
+    for (int g0 = s; g0 < G; g0 += 32) {
+        float a8[8];
+        int c8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const size_t at = size_t(row) * G + min(g0 + 4 * u, G - 1);
+            a8[u] = p.as[at];
+            c8[u] = p.corr[at];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int g = g0 + 4 * u;
+            if (g < G) {
+                tsc[g * 16 + i] = a8[u];
+                tco[g * 16 + i] = c8[u];
+            }
+        }
+    }
+    __syncthreads();
+
+    auto fetch = [&](int g, T2Stage16 &st) {
+        st.a[0] = *reinterpret_cast<const v2l *>(arow + g * 128);
+        st.a[1] = *reinterpret_cast<const v2l *>(arow + g * 128 + 64);
+        st.w[0] = *reinterpret_cast<const int2 *>(wcol + size_t(4 * g + (s >> 1)) * 32);
+        st.w[1] = *reinterpret_cast<const int2 *>(wcol + size_t(4 * g + 2 + (s >> 1)) * 32);
+        st.ws = wscol[size_t(g) * 4];
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](int g, const T2Stage16 &st) {
+        v4i d = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int sh = 4 * (s & 1) + 2 * (j & 1);
+            const int2 wd = st.w[j >> 1];
+            const int lo = (wd.x >> sh) & 0x03030303, hi = (wd.y >> sh) & 0x03030303;
+            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.a[j >> 1][j & 1], long(unsigned(lo)) | (long(hi) << 32), d, 0, 0, 0);
+        }
+        const v4f sc = *reinterpret_cast<const v4f *>(tsc + g * 16 + 4 * s);
+        const v4i co = *reinterpret_cast<const v4i *>(tco + g * 16 + 4 * s);
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float D = float(co[v] + d[v]);
+            acc[v] = FUSED ? __builtin_fmaf(D, st.ws * sc[v], acc[v]) : acc[v] + D * (st.ws * sc[v]);
+        }
+    };
+
+    // group g lives in stage g % kT2Gemm16Depth; its refill (clamped at the last group, so no
+    // branch splits the loads) follows its rescale
+    T2Stage16 st[kT2Gemm16Depth];
+#pragma unroll
+    for (int k = 0; k < kT2Gemm16Depth; k++) {
+        fetch(min(k, G - 1), st[k]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int g = 0; g < G; g += kT2Gemm16Depth) {
+#pragma unroll
+        for (int k = 0; k < kT2Gemm16Depth; k++) {
+            if (g + k < G) step(g + k, st[k]);
+            fetch(min(g + k + kT2Gemm16Depth, G - 1), st[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const int n = n0 + i;
+    if (n >= col_begin + ncol) return;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int r = m0 + 4 * s + v;
+        if (r >= p.rows) continue;
+        float y = acc[v];
+        if (p.bias && n < p.n_rows) y = y + p.bias[n];
+        float *o = p.out + size_t(r) * p.ld_out + (n - col_begin);
+        *o = p.accumulate ? *o + y : y;
+    }
+}
+
+template <bool FUSED>
+int launch_t2_gemm16(const T2Params &p, hipStream_t s)
+{
+    const long tiles = long((p.quad_end - p.quad_begin) * 4 + 15) / 16 * ((p.rows + 15) / 16);
+    t2_gemm16_kernel<FUSED><<<unsigned(tiles), 64, size_t(p.G) * 16 * 8, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
 }
 
 template <int R, bool FUSED>
@@ -1662,7 +1791,9 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
     // the matrix cores for many rows, the streamed kernel for few (the int32 dots stay on the
     // one-thread-per-output kernel)
     const bool fused = a.fused != 0;
-    if (rc == FG_OK && !a.dots && M >= kT2GemmRows && size_t(G) * 32 * 8 <= 64 * 1024 && (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
+    const bool tiles16 = M >= kT2Gemm16Rows && M <= 16;
+    if (rc == FG_OK && !a.dots && (tiles16 || M >= kT2GemmRows) && size_t(G) * 32 * 8 <= 64 * 1024 &&
+        (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
         T2Params p{};
         p.codes = reinterpret_cast<const uint8_t *>(t->codes);
         p.wscales = t->scales;
@@ -1681,7 +1812,10 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         p.out = a.out;
         p.ld_out = long(a.ld_out);
         p.accumulate = a.accumulate;
-        rc = fused ? launch_t2_gemm<true>(p, s) : launch_t2_gemm<false>(p, s);
+        if (tiles16)
+            rc = fused ? launch_t2_gemm16<true>(p, s) : launch_t2_gemm16<false>(p, s);
+        else
+            rc = fused ? launch_t2_gemm<true>(p, s) : launch_t2_gemm<false>(p, s);
         if (owned) {
             hipError_t e = hipFreeAsync(ws, s);
             if (rc == FG_OK && e != hipSuccess) rc = check_hip(e, "hipFreeAsync");

@@ -396,7 +396,8 @@ def test_int4_shape_bit_exact(fk, rows):
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128), (5, 16384)])
 def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
-    """The streamed T2b128 kernel (up to 8 rows): 3 groups (one partial 1 KiB chunk), 9 groups (a
+    """T2b128 products of up to 8 rows (the streamed kernel up to 4, the 16 x 16 matrix-core tiles
+    from 5): 3 groups (one partial 1 KiB chunk), 9 groups (a
     second chunk of one group), 40 groups (five chunks: the four-chunk ring refilled), one group,
     and 128 groups (16384 levels a row: slices of two rows, not four or eight, to fit the
     workgroup's LDS); slices of 1, 2, 4 or 8 rows; 70 outputs (a last workgroup of two quads);
@@ -425,7 +426,7 @@ def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
 @pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128)])
 def test_t2_on_the_matrix_cores(fk, rows, n_rows, cols):
     """T2b128 products of 9 or more rows (the int8 matrix cores, a group's four blocks chained in
-    one accumulator): 3, 9, 40 and 1 groups (odd counts against the two-group ring), partial row
+    one accumulator; 16 x 16 tiles up to 16 rows, 32 x 32 or 32 x 64 past them): 3, 9, 40 and 1 groups (odd counts against the two-group ring), partial row
     tiles (9, 31, 33, 100 rows) and column tiles (70 outputs), bias, the fused scaling, a column
     range, pre-quantized rows."""
     print(f"t2 mfma {rows} x {cols} -> {n_rows}", flush=True)

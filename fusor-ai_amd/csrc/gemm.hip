@@ -1520,6 +1520,12 @@ constexpr int kT2Gemm16Depth = 4;  // groups in flight
 #define FG_T2_MFMA16_ROWS 5
 #endif
 constexpr int kT2Gemm16Rows = FG_T2_MFMA16_ROWS;  // fewest rows taken by the 16 x 16 kernel
+#ifndef FG_T2_MFMA16_MAX_ROWS
+#define FG_T2_MFMA16_MAX_ROWS 16
+#endif
+// most rows taken by it: for 17-32 rows two row tiles of 16 x 16 measured 24.5 µs against
+// 17.4-19.6 for one of 32 x 32
+constexpr int kT2Gemm16MaxRows = FG_T2_MFMA16_MAX_ROWS;
 
 typedef long v2l __attribute__((ext_vector_type(2)));
 struct T2Stage16 {
@@ -1791,7 +1797,7 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
     // the matrix cores for many rows, the streamed kernel for few (the int32 dots stay on the
     // one-thread-per-output kernel)
     const bool fused = a.fused != 0;
-    const bool tiles16 = M >= kT2Gemm16Rows && M <= 16;
+    const bool tiles16 = M >= kT2Gemm16Rows && M <= kT2Gemm16MaxRows;
     if (rc == FG_OK && !a.dots && (tiles16 || M >= kT2GemmRows) && size_t(G) * 32 * 8 <= 64 * 1024 &&
         (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
         T2Params p{};

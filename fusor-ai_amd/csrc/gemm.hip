@@ -1734,10 +1734,13 @@ ScratchPlan plan_scratch(const ProductArgs &a)
     const size_t M = a.rows, K = t->cols, G = t->groups;
     ScratchPlan pl{};
     pl.q_bytes = a.x ? (M * K + 255) / 256 * 256 : 0;
-    pl.s_bytes = a.x ? (M * G * 4 + 255) / 256 * 256 : 0;
+    // f32 rows quantized into row-major scales and corrections (quantize_rows), unless they go
+    // straight into the block-major copy (then no row-major scales are written)
+    const size_t row_scales = a.x ? (M * G * 4 + 255) / 256 * 256 : 0;
     pl.Mpad = int((M + 63) / 64 * 64);
     if (t->dtype == FG_T2B128) {
         pl.lds = true;
+        pl.s_bytes = row_scales;
         return pl;
     }
     pl.tiles = choose_tiles(a);
@@ -1753,6 +1756,7 @@ ScratchPlan plan_scratch(const ProductArgs &a)
     const bool dots = a.dots != nullptr;
     pl.lds = !dots && G * 32 * 4 <= 64 * 1024 && G % 4 == 0 && (a.x || (reinterpret_cast<uintptr_t>(a.as) & 15) == 0);
     pl.t_bytes = (pl.lds || dots) ? 0 : G * size_t(pl.Mpad) * 4;
+    pl.s_bytes = pl.t_bytes ? 0 : row_scales;
     return pl;
 }
 
@@ -1828,7 +1832,9 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         }
         return rc;
     }
-    int R = M >= 5 ? 8 : M >= 3 ? 4 : M;
+    // slices of up to four rows (5-16 rows take the 16 x 16 tiles above unless the groups are too
+    // many for them, and then the levels of four rows already overflow the LDS)
+    int R = M >= 3 ? 4 : M;
     while (R > 1 && t2_lds_bytes(R, K, G, fused) > 64 * 1024) R /= 2;
     if (rc == FG_OK && !a.dots && M > 0 && t2_lds_bytes(R, K, G, fused) <= 64 * 1024 && (reinterpret_cast<uintptr_t>(q) & 15) == 0 &&
         (M + R - 1) / R <= 65535) {
@@ -1850,8 +1856,7 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
         p.out = a.out;
         p.ld_out = long(a.ld_out);
         p.accumulate = a.accumulate;
-        rc = R == 8   ? launch_t2_rows<8>(p, fused, s)
-             : R == 4 ? launch_t2_rows<4>(p, fused, s)
+        rc = R == 4   ? launch_t2_rows<4>(p, fused, s)
              : R == 2 ? launch_t2_rows<2>(p, fused, s)
                       : launch_t2_rows<1>(p, fused, s);
     } else if (rc == FG_OK) {

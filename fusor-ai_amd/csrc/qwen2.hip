@@ -664,8 +664,8 @@ int residual_launch(fg_qwen2 *m, const fg_table *t, int in, hipStream_t st, size
     return launch_proj(p, m->shape.dtype, in, OUT_STORE, m->shape.exact != 0, st);
 }
 
-// 4. RMSNorm -> gate and up -> silu(gate)·up.
-int swiglu_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, hipStream_t st)
+// 4. RMSNorm -> gate and up -> silu(gate)·up (also to act_out, f32, when set).
+int swiglu_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, hipStream_t st, float *act_out = nullptr)
 {
     const fg_qwen2_shape &sh = m->shape;
     ProjParams p = table_params(ly.gate);
@@ -679,6 +679,7 @@ int swiglu_launch(fg_qwen2 *m, const fg_qwen2_layer &ly, hipStream_t st)
     p.q_out = m->xq;
     p.s_out = m->xs;
     p.c_out = m->xc;
+    p.act_out = act_out;
     return launch_proj(p, sh.dtype, IN_NORM, OUT_SWIGLU, sh.exact != 0, st);
 }
 
@@ -703,7 +704,13 @@ int attention_launch(fg_qwen2 *m, size_t li, size_t position, hipStream_t st, fl
     a.row_out = row_out;
     const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims));
     if (prescored_attention(m)) {
-        // the cached keys' scores come from the query launch; the softmax and ordered weighted sums
+        // the cached keys' scores come from the query launch; the softmax and ordered weighted sums.
+        // Past the default 64 KiB of LDS the kernel's limit is raised to the CU's 160 KiB on the
+        // current device before each launch (a host call with no stream work), as the projection
+        // and the batched product do: no per-model value that another model could lower.
+        const void *f = sh.head_dim == 64 ? reinterpret_cast<const void *>(attn_exact_kernel<64>)
+                                          : reinterpret_cast<const void *>(attn_exact_kernel<128>);
+        if (m->exact_smem > 64 * 1024) FG_HIP(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         if (sh.head_dim == 64) attn_exact_kernel<64><<<wgrid, kAttnThreads, m->exact_smem, st>>>(a);
         else attn_exact_kernel<128><<<wgrid, kAttnThreads, m->exact_smem, st>>>(a);
         FG_HIP(hipGetLastError());
@@ -814,15 +821,6 @@ extern "C" int fg_qwen2_create(const fg_qwen2_shape *shape, const fg_qwen2_layer
         delete m;
         return set_error(FG_ERR_SHAPE, "fg_qwen2_create: the attention does not fit (heads per KV head x head_dim <= 1024, capacity)");
     }
-    if (sh.exact && (D == 64 || D == 128)) {
-        // the one-launch exact attention takes more LDS than the default limit
-        const void *f = D == 64 ? reinterpret_cast<const void *>(attn_exact_kernel<64>) : reinterpret_cast<const void *>(attn_exact_kernel<128>);
-        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, int(m->exact_smem));
-        if (e != hipSuccess) {
-            delete m;
-            return set_error(FG_ERR_HIP, std::string("fg_qwen2_create: ") + hipGetErrorString(e));
-        }
-    }
     const size_t widest = std::max(sh.hidden, std::max(width, sh.ffn));
     const size_t padded_vocab = table->quads * 4;
     struct Alloc {
@@ -906,6 +904,44 @@ extern "C" int fg_qwen2_attention(fg_qwen2 *m, size_t layer, size_t position, co
         if ((rc = attention_launch(m, layer, position, st, row))) return rc;
     }
     FG_HIP(hipMemcpyAsync(query, m->qkv, sh.heads * sh.head_dim * 4, hipMemcpyDeviceToDevice, st));
+    return FG_OK;
+}
+
+extern "C" int fg_qwen2_layer_probe(fg_qwen2 *m, size_t layer, size_t position, const float *hidden,
+                                    const fg_qwen2_probe *probe, void *stream)
+{
+    if (!m || !hidden || !probe) return set_error(FG_ERR_ARG, "fg_qwen2_layer_probe: a null argument");
+    if (layer >= m->shape.layers || position >= m->shape.capacity)
+        return set_error(FG_ERR_SHAPE, "fg_qwen2_layer_probe: layer or position out of range");
+    const fg_qwen2_shape &sh = m->shape;
+    const fg_qwen2_layer &ly = m->layers[layer];
+    const size_t width = sh.heads * sh.head_dim, groups = sh.ffn / 32;
+    hipStream_t st = as_stream(stream);
+    auto copy = [&](void *to, const void *from, size_t bytes) -> hipError_t {
+        return to ? hipMemcpyAsync(to, from, bytes, hipMemcpyDeviceToDevice, st) : hipSuccess;
+    };
+    FG_HIP(hipMemcpyAsync(m->hidden, hidden, sh.hidden * 4, hipMemcpyDeviceToDevice, st));
+    int rc;
+    // attention and the output projection, as run_layer runs them (the attention row captured by
+    // the launch that forms it)
+    if (fast_attention(m)) {
+        if ((rc = qattn_launch(m, ly, layer, position, st))) return rc;
+        if ((rc = residual_launch(m, ly.o, IN_ATTN, st, layer, position, probe->attention))) return rc;
+    } else {
+        if ((rc = prescored_attention(m) ? qattn_launch(m, ly, layer, position, st) : qkv_launch(m, ly, layer, position, st)))
+            return rc;
+        if ((rc = attention_launch(m, layer, position, st, probe->attention))) return rc;
+        if ((rc = residual_launch(m, ly.o, IN_PREQ, st))) return rc;
+    }
+    FG_HIP(copy(probe->query, m->qkv, width * 4));
+    FG_HIP(copy(probe->attended, m->hidden, sh.hidden * 4));
+    // the feed-forward: silu(gate)·up captured by its epilogue, then the row it quantized for down
+    if ((rc = swiglu_launch(m, ly, st, probe->inner))) return rc;
+    FG_HIP(copy(probe->levels, m->xq, sh.ffn));
+    FG_HIP(copy(probe->scales, m->xs, groups * 4));
+    FG_HIP(copy(probe->corrections, m->xc, groups * 4));
+    if ((rc = residual_launch(m, ly.down, IN_PREQ, st))) return rc;
+    FG_HIP(copy(probe->out, m->hidden, sh.hidden * 4));
     return FG_OK;
 }
 

@@ -43,6 +43,11 @@ class FgQwen2Layer(ctypes.Structure):
                 ("gate", _P), ("up", _P), ("down", _P)]
 
 
+class FgQwen2Probe(ctypes.Structure):
+    _fields_ = [("query", _P), ("attention", _P), ("attended", _P), ("inner", _P), ("levels", _P),
+                ("scales", _P), ("corrections", _P), ("out", _P)]
+
+
 # Every symbol include/fusor_gpu.h declares, with its signature.
 SIGNATURES = {
     "fg_last_error": (ctypes.c_char_p, []),
@@ -74,6 +79,7 @@ SIGNATURES = {
     "fg_qwen2_step": (_I, [_P, _I, _S, _P, _P, _P, _P]),
     "fg_qwen2_layer_forward": (_I, [_P, _S, _S, _P, _P]),
     "fg_qwen2_attention": (_I, [_P, _S, _S, _P, _P, _P, _P]),
+    "fg_qwen2_layer_probe": (_I, [_P, _S, _S, _P, ctypes.POINTER(FgQwen2Probe), _P]),
     "fg_qwen2_free": (_I, [_P]),
 }
 

@@ -9,7 +9,7 @@ import ctypes
 from dataclasses import dataclass
 
 from . import _lib
-from ._lib import FgQwen2Layer, FgQwen2Shape, check, lib, ptr, stream_handle
+from ._lib import FgQwen2Layer, FgQwen2Probe, FgQwen2Shape, check, lib, ptr, stream_handle
 
 
 @dataclass
@@ -69,3 +69,24 @@ class Qwen2:
         heads * head_dim); the position's key and value are kept in the caches."""
         check(lib().fg_qwen2_attention(self.handle, layer, position, ptr(hidden), ptr(query), ptr(row),
                                        stream_handle(stream)))
+
+    def probe(self, layer, position, hidden, stream=None):
+        """One layer over `hidden` as the step runs it, returning what it forms on the way (an
+        inspection): the rotated query heads, the attention row before the output projection
+        quantizes it, the residual row after that projection, silu(gate)·up, its levels, scales and
+        corrections for the down projection, and the layer's output row (device tensors)."""
+        import torch
+        sh = self.shape
+        dev = hidden.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        out = {"query": torch.empty(sh.width(), **f32), "attention": torch.empty(sh.width(), **f32),
+               "attended": torch.empty(sh.hidden, **f32), "inner": torch.empty(sh.ffn, **f32),
+               "levels": torch.empty(sh.ffn, dtype=torch.int8, device=dev),
+               "scales": torch.empty(sh.ffn // 32, **f32),
+               "corrections": torch.empty(sh.ffn // 32, dtype=torch.int32, device=dev),
+               "out": torch.empty(sh.hidden, **f32)}
+        pr = FgQwen2Probe(*(ptr(out[k]) for k in ("query", "attention", "attended", "inner", "levels", "scales",
+                                                  "corrections", "out")))
+        check(lib().fg_qwen2_layer_probe(self.handle, layer, position, ptr(hidden), ctypes.byref(pr),
+                                         stream_handle(stream)))
+        return out

@@ -9,8 +9,11 @@
  * the last failure on the calling thread is fg_last_error(). No call retains a caller pointer
  * after it returns, except the table and model handles, which own their device memory.
  *
- * Calls are thread-safe: the reference calls the product from every thread of a team
- * (linear.rs:113-143); concurrent calls on disjoint outputs are independent.
+ * Calls are thread-safe, except fg_matmul_noalloc: the reference calls the product from every
+ * thread of a team (linear.rs:113-143), and concurrent fg_matmul calls on disjoint outputs are
+ * independent. fg_matmul_noalloc shares one scratch array per device among all its calls, so its
+ * calls that overlap on a device race and must be serialized by the caller. One model handle
+ * (fg_qwen2) or upload (fg_upload) is used by one thread at a time.
  */
 #ifndef FUSOR_GPU_H
 #define FUSOR_GPU_H
@@ -194,9 +197,11 @@ int fg_matmul(const fg_table *table, const fg_input *input, size_t rows, size_t 
  * scratch): it is for callers that cannot allocate device memory, such as code under HIP graph
  * capture or a serving loop that forbids hipMalloc. Products that quantize f32 rows on the matrix
  * cores (5 or more rows, or T2b128) need scratch for the levels, scales and corrections; here it is
- * a fixed array of 32 MiB per device, held by the library from its load until the process ends
- * (rows * cols + 8 * rows * groups bytes, each part rounded up to 256, must fit; larger products
- * return FG_ERR_SHAPE and belong to fg_matmul). Nothing in the array needs to start at zero: every
+ * a fixed array of 32 MiB per device, held by the library from its load until the process ends.
+ * A product needs rows * cols bytes of levels plus at most 8 * (rows + 127) * groups bytes of scales
+ * and corrections (row-major scales and corrections, 8 * rows * groups, or the block-major scales of
+ * the staged kernel, 4 * groups * rows rounded up to 128 rows), each part rounded up to 256 bytes;
+ * larger products return FG_ERR_SHAPE and belong to fg_matmul. Nothing in the array needs to start at zero: every
  * call writes what it reads. All calls on one device share the array, so calls that overlap on a
  * device (other threads or streams) race: serialize them. FG_PARALLEL_SUM is not taken. */
 int fg_matmul_noalloc(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
@@ -247,6 +252,26 @@ int fg_qwen2_layer_forward(fg_qwen2 *model, size_t layer, size_t position, float
  * changed. */
 int fg_qwen2_attention(fg_qwen2 *model, size_t layer, size_t position, const float *hidden, float *query,
                        float *row, void *stream);
+
+/* What one layer forms on the way (layer.rs:161-344), each written by the launch that forms it:
+ * device outputs, any may be NULL. */
+typedef struct {
+    float *query;         /* [heads * head_dim]: the rotated query heads (layer.rs:175-209) */
+    float *attention;     /* [heads * head_dim]: the attention row before the output projection
+                             quantizes it (transformer.rs:185-219) */
+    float *attended;      /* [hidden]: the residual row after the output projection (layer.rs:239-245) */
+    float *inner;         /* [ffn]: silu(gate) * up (layer.rs:298-344) */
+    int8_t *levels;       /* [ffn]: that row quantized for the down projection (quantize_rows) */
+    float *scales;        /* [ffn / 32] */
+    int32_t *corrections; /* [ffn / 32] */
+    float *out;           /* [hidden]: the layer's output row (layer.rs:269-291) */
+} fg_qwen2_probe;
+
+/* One layer over a device hidden row as the step runs it, with its intermediate rows written to
+ * `probe` (an inspection for layer-level parity checks): the position's key and value are kept in
+ * the caches, `hidden` is not changed. */
+int fg_qwen2_layer_probe(fg_qwen2 *model, size_t layer, size_t position, const float *hidden,
+                         const fg_qwen2_probe *probe, void *stream);
 int fg_qwen2_free(fg_qwen2 *model);
 
 #ifdef __cplusplus

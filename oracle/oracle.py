@@ -264,6 +264,21 @@ def rope_tables(base, head_dim, positions):
     return cos, sin
 
 
+def rope_half(head, cos, sin):
+    """ops::rope by halves (ops.rs:77-85) of one head: a rotated copy."""
+    head = np.array(head, dtype=np.float32)
+    cos = np.ascontiguousarray(cos, dtype=np.float32)
+    sin = np.ascontiguousarray(sin, dtype=np.float32)
+    assert cos.size == sin.size == head.size // 2
+    lib().or_rope_half(_ptr(head), head.size, _ptr(cos), _ptr(sin))
+    return head
+
+
+def silu_rows(x):
+    """silu (ops.rs:272-274) of every value."""
+    return np.array([silu(v) for v in np.asarray(x, np.float32).reshape(-1)], np.float32)
+
+
 def dot_f32(a, b):
     """dot_f32 (arch/scalar.rs:340-342): the products added in index order."""
     a = np.ascontiguousarray(a, dtype=np.float32)

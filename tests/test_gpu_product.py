@@ -396,12 +396,11 @@ def test_int4_shape_bit_exact(fk, rows):
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128), (5, 16384)])
 def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
-    """T2b128 products of up to 8 rows (the streamed kernel up to 4, the 16 x 16 matrix-core tiles
-    from 5): 3 groups (one partial 1 KiB chunk), 9 groups (a
+    """T2b128 products of up to 8 rows: 1-4 rows on the streamed kernel (slices of 1, 2 or 4 rows),
+    5 and 8 rows on the 16 x 16 matrix-core tiles; 3 groups (one partial 1 KiB chunk), 9 groups (a
     second chunk of one group), 40 groups (five chunks: the four-chunk ring refilled), one group,
-    and 128 groups (16384 levels a row: slices of two rows, not four or eight, to fit the
-    workgroup's LDS); slices of 1, 2, 4 or 8 rows; 70 outputs (a last workgroup of two quads);
-    bias and the fused scaling."""
+    and 128 groups (16384 levels a row: slices of two rows, not four, to fit the workgroup's LDS);
+    70 outputs (a last workgroup of two quads); bias and the fused scaling."""
     print(f"t2 {rows} x {cols} -> {n_rows}", flush=True)
     dtype = O.T2B128
     data = synthetic_table(dtype, n_rows, cols, seed=n_rows + cols + rows)

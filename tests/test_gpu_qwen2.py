@@ -294,10 +294,12 @@ def test_decoder_rejects_positions_past_the_cache(fk):
 
 
 @pytest.mark.parametrize("exact", [True, False])
-def test_qwen2_half_billion_shape_at_position_511(fk, exact):
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+def test_qwen2_half_billion_shape_at_position_511(fk, exact, dtype):
     """The Qwen2-0.5B-shaped step (hidden 896, 24 layers, 14/2 heads of 64, FFN 4864, vocabulary
-    151936) at position 511 over a cache of N(0,1) keys and values."""
-    dtype = O.Q7B32
+    151936) at position 511 over a cache of N(0,1) keys and values, with 7-bit and 4-bit tables
+    (the reference's LM layers run Q4b32: models/ming/compile/src/lib.rs:49-56)."""
+    print(f"Qwen2-0.5B shape dtype {dtype} exact {exact}", flush=True)
     params = build(dtype, hidden=896, layers=24, heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=151936,
                    capacity=512, seed=11, synthetic=True)
     got, want = run_both(fk, dtype, params, token=1234, position=511, exact=exact)
@@ -313,7 +315,7 @@ def test_qwen2_half_billion_shape_at_position_511(fk, exact):
         sh, lys, final, table, kc, vc = params
         model = O.Qwen2(sh, lys, final, table)
         cos, sin = O.rope_tables(sh.rope_base, sh.head_dim, sh.capacity)
-        h = O.dequantize_row(O.Q7B32, sh.vocab, sh.hidden, table, 1234)
+        h = O.dequantize_row(dtype, sh.vocab, sh.hidden, table, 1234)
         hp = (h * (1 + 1e-6 * np.random.default_rng(0).standard_normal(sh.hidden))).astype(np.float32)
         k1, v1, k2, v2 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
         for layer in range(sh.layers):

@@ -106,6 +106,41 @@ def test_upload_errors_and_restart(fk):
         fk.TableUpload(O.T2B128, [4, 64])
 
 
+def test_restart_after_staging_flushes(fk):
+    """A restart once more than one 8 MiB staging buffer has gone to the device (copies in flight,
+    codes already re-laid out, the second buffer in use): a 4864 x 2048 Q7b32 table (10.0 MB) written
+    whole, restarted, then written again in ragged pieces; and the same through a Store's
+    restart_part (store.rs:148-158) on a part holding that table and a bias."""
+    rows, cols = 4864, 2048
+    print(f"upload restart after flushes {rows} x {cols}", flush=True)
+    data = synthetic_table(O.Q7B32, rows, cols, seed=21)
+    rng = np.random.default_rng(22)
+    up = fk.TableUpload(O.Q7B32, [rows, cols])
+    up.write(data[: 9 << 20])
+    up.write(data[9 << 20:])
+    up.restart()
+    for at, size in pieces(data.size, rng):
+        up.write(data[at:at + size])
+    check_table(fk, up.end(), O.Q7B32, rows, cols, data, row_sets=(1, 17))
+
+    bias = rng.standard_normal(rows).astype(np.float32)
+    other = synthetic_table(O.Q7B32, rows, cols, seed=23)  # the first attempt's bytes differ
+    part = data.tobytes() + bias.tobytes()
+    manifest = {"parts": [{"file": "w.bin", "bytes": len(part)}],
+                "tensors": {"w": {"dtype": O.Q7B32, "shape": [rows, cols], "part": 0, "offset": 0},
+                            "b": {"dtype": 0, "shape": [rows], "part": 0, "offset": data.size}}}
+    store = fk.Store(manifest)
+    first = other.tobytes() + bias.tobytes()
+    for at, size in pieces(len(first) - 1000, rng):
+        store.write(0, first[at:at + size])
+    store.restart_part(0)
+    for at, size in pieces(len(part), rng):
+        store.write(0, part[at:at + size])
+    store.end_part(0)
+    check_table(fk, store.take("w"), O.Q7B32, rows, cols, data, row_sets=(1,))
+    assert np.array_equal(store.take("b").bytes(), bias.view(np.uint8))
+
+
 def test_store_streams_a_bundle_into_device_tables(fk):
     """compile/src/writer.rs:117-152 through the device: one part holding an f32 norm and a
     Q7b32 weight back to back, a blob part, every part pushed in 7-byte writes; then a second

@@ -61,6 +61,29 @@ def test_noalloc_equals_the_allocating_product_twice_in_a_row(fk, dtype):
         assert same_bits(got.cpu().numpy(), oracle), (rows, k, n)
 
 
+def test_noalloc_on_the_staged_kernel(fk):
+    """Products on the LDS-staged kernel, whose f32 rows are quantized straight into block-major
+    scales (no row-major scales or corrections in the scratch): 6144 x 4096 -> 4096 needs 24 MiB of
+    levels and 3 MiB of scales, then a smaller call. Bit for bit against fg_matmul on every row and
+    against the oracle on the first rows (rows are independent)."""
+    import torch
+    dtype = O.Q8B32
+    for rows, k, n in [(6144, 4096, 4096), (512, 4096, 4096)]:
+        print(f"noalloc staged {rows} x {k} -> {n}", flush=True)
+        data = synthetic_table(dtype, n, k, seed=rows + 1)
+        t = fk.Table(fk.Tensor(dtype, [n, k], data))
+        xh = activations(rows, k, seed=rows + 2, outliers=0.01)
+        x = torch.from_numpy(xh.reshape(-1)).cuda()
+        want = fk.matmul(t.matrix(), fk.Input(f32=x), range(0, n))
+        got = noalloc(fk, t, x, rows, n)
+        torch.cuda.synchronize()
+        got_h = got.cpu().numpy()
+        assert same_bits(got_h, want.cpu().numpy()), (rows, k, n)
+        head = 16
+        q, s, c = O.quantize_rows(xh[:head].reshape(-1), dtype)
+        assert same_bits(got_h[:head], O.matmul(dtype, n, k, data, q, s, c, head)), (rows, k, n)
+
+
 def test_noalloc_accumulates_and_takes_the_fused_scale(fk):
     import torch
     from fusor_kernels import _lib

@@ -399,6 +399,8 @@ int table_alloc(int dtype, size_t rows, size_t cols, fg_table **out);
 size_t table_byte_len(int dtype, size_t rows, size_t cols);
 int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint8_t *bytes, hipStream_t s);
 int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s);
+// The table's rows ids[0..count) (device ids) into out[count][cols].
+int launch_embed_rows(const fg_table *t, const int32_t *ids, size_t count, float *out, hipStream_t s);
 // quantize_rows for groups of 32 with the scales written block-major, as_t[g][Mpad] (zeros for the
 // rows past `rows`), and no corrections: the form the batched product's kernels read.
 int launch_quantize_rows_t(const float *x, size_t rows, size_t K, int dtype, int8_t *q, float *as_t, size_t Mpad,

@@ -66,7 +66,35 @@ __global__ __launch_bounds__(kThreads) void norm_quantize_kernel(ProjParams p)
     stage_finish<8, 1, IN_NORM, EXACT>(p, g, p.q_out, p.s_out, p.c_out, nbuf, red);
 }
 
+// The same over rows: workgroup y takes row y of x [rows][K] into its levels [rows][K], scales and
+// corrections [rows][G].
+template <bool EXACT>
+__global__ __launch_bounds__(kThreads) void norm_quantize_rows_kernel(ProjParams p)
+{
+    __shared__ __align__(16) float nbuf[4 * 4 * kThreads];
+    __shared__ float red[16];
+    const size_t y = blockIdx.x;
+    p.x += y * p.K;
+    p.q_out += y * p.K;
+    p.s_out += y * p.G;
+    p.c_out += y * p.G;
+    StageRegs g;
+    stage_issue<8, 1, IN_NORM>(p, g);
+    stage_finish<8, 1, IN_NORM, EXACT>(p, g, p.q_out, p.s_out, p.c_out, nbuf, red);
+}
+
 }  // namespace
+
+int launch_norm_quantize_rows(const ProjParams &p, int rows, bool exact, hipStream_t s)
+{
+    if (p.K % 32 || p.K > 4 * 4 * kThreads || p.G * 32 != p.K)
+        return set_error(FG_ERR_SHAPE, "the RMSNorm prologue takes rows of at most 4096");
+    if (rows <= 0) return FG_OK;
+    if (exact) norm_quantize_rows_kernel<true><<<unsigned(rows), kThreads, 0, s>>>(p);
+    else norm_quantize_rows_kernel<false><<<unsigned(rows), kThreads, 0, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
 
 int launch_norm_quantize(const ProjParams &p, bool exact, hipStream_t s)
 {

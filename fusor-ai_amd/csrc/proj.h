@@ -143,5 +143,7 @@ __device__ __forceinline__ float ref_silu(float x) { return x / (1.0f + ref_exp(
 size_t proj_smem(const ProjParams &p, int rows, int in, int out);
 int launch_proj(const ProjParams &p, int dtype, int in, int out, bool exact, hipStream_t s);
 int launch_norm_quantize(const ProjParams &p, bool exact, hipStream_t s);
+// The same for `rows` rows: x [rows][K] to q_out [rows][K], s_out and c_out [rows][G].
+int launch_norm_quantize_rows(const ProjParams &p, int rows, bool exact, hipStream_t s);
 
 }  // namespace fg

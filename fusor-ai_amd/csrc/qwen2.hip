@@ -50,16 +50,36 @@ struct AttnParams {
     float *scales;
     int32_t *corr;
     float *row_out;  // when set, the f32 attention row before its quantization (an inspection)
+    // rows of a prefill (grid z): row z's query heads at qkv + z·qkv_stride, its scores [heads][capacity]
+    // after z such blocks, its outputs (levels, scales, corrections, row_out) z·row_width values on, and
+    // keys + z keys (its own position's included)
+    size_t qkv_stride, row_width;
 };
+
+// Row blockIdx.z of a prefill's attention: its own query, scores, outputs and key count.
+__device__ __forceinline__ void attn_row(AttnParams &a)
+{
+    const size_t z = blockIdx.z;
+    if (z == 0) return;
+    a.qkv += z * a.qkv_stride;
+    a.scores += z * size_t(a.heads) * a.capacity;
+    a.keys += int(z);
+    a.q += z * a.row_width;
+    a.scales += z * a.row_width / 32;
+    a.corr += z * a.row_width / 32;
+    if (a.row_out) a.row_out += z * a.row_width;
+}
 
 // Scores of every query head of one KV head against kScoreKeys keys (ops.rs:310-326):
 // dot_f32(q, k_j) in index order, times 1/√D. Grid: (kv_heads, key blocks).
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnParams a)
 {
     extern __shared__ __align__(16) float ash[];
+    attn_row(a);
     const int D = a.D, S = D + 1;
     const int group = a.heads / a.kv_heads;
     const int kv = blockIdx.x, j0 = int(blockIdx.y) * kScoreKeys;
+    if (j0 >= a.keys) return;  // a prefill's earlier rows see fewer keys (uniform per workgroup)
     const int n = min(kScoreKeys, a.keys - j0);
     float *krows = ash;                      // [kScoreKeys][D + 1]
     float *query = krows + kScoreKeys * S;   // [group][D]
@@ -154,6 +174,7 @@ template <bool EXACT>
 __global__ __launch_bounds__(kAttnThreads) void attn_weigh_kernel(AttnParams a)
 {
     extern __shared__ __align__(16) float ash[];
+    attn_row(a);
     constexpr int S = kWeighDims + 1;
     const int D = a.D, keys = a.keys;
     const int head = blockIdx.x, d0 = int(blockIdx.y) * kWeighDims;
@@ -469,6 +490,63 @@ __global__ __launch_bounds__(kAttnThreads) void attn_exact_kernel(AttnParams a)
     }
 }
 
+// A prefill's rotary embeddings and kept rows: row r's query and key heads rotated by halves at
+// position first + r (ops.rs:77-85, the row's own angles), its key and value heads kept at that
+// position (KvCache::keep, transformer.rs:166-180). Grid: (rows, heads + 2·kv_heads), D/2 threads.
+__global__ void rope_keep_rows_kernel(float *__restrict__ qkv, size_t stride, const float *__restrict__ rope, int heads,
+                                      int kv_heads, int D, float *__restrict__ kcache, float *__restrict__ vcache,
+                                      size_t layer_base, int capacity, int first)
+{
+    const int r = int(blockIdx.x), unit = int(blockIdx.y), j = int(threadIdx.x), half = D / 2;
+    if (j >= half) return;
+    float *head = qkv + size_t(r) * stride + size_t(unit) * D;
+    const int position = first + r;
+    float x = head[j], y = head[j + half];
+    if (unit < heads + kv_heads) {
+        const float *cs = rope + size_t(position) * D;  // cos[half] then sin[half]
+        const float c = cs[j], sn = cs[half + j];
+        const float nx = x * c - y * sn;
+        const float ny = y * c + x * sn;
+        x = nx;
+        y = ny;
+        head[j] = x;
+        head[j + half] = y;
+    }
+    if (unit >= heads) {
+        const bool key = unit < heads + kv_heads;
+        const int kv = (unit - heads) % kv_heads;
+        float *cache = key ? kcache : vcache;
+        const size_t at = layer_base + (size_t(kv) * capacity + size_t(position % capacity)) * D;
+        cache[at + j] = x;
+        cache[at + j + half] = y;
+    }
+}
+
+// silu(gate)·up of a prefill's rows (layer.rs:321-341), quantized per group of 32 for the down
+// projection with quantize_rows' arithmetic: 8 lanes per group, four values per lane.
+__global__ void swiglu_quantize_kernel(const float *__restrict__ gate, const float *__restrict__ up, size_t groups, int zp,
+                                       int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ corr)
+{
+    const size_t t = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t g = t / 8;
+    const int sub = int(t % 8);
+    const bool active = g < groups;
+    const size_t at = active ? g * 8 + sub : 0;
+    const float4 a = reinterpret_cast<const float4 *>(gate)[at], b = reinterpret_cast<const float4 *>(up)[at];
+    const float4 v = make_float4(ref_silu(a.x) * b.x, ref_silu(a.y) * b.y, ref_silu(a.z) * b.z, ref_silu(a.w) * b.w);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = max8(fmaxf(0.0f, amax));
+    int l0, l1, l2, l3;
+    const float d = scale_and_levels(amax, v.x, v.y, v.z, v.w, l0, l1, l2, l3);
+    const int sum = sum8(l0 + l1 + l2 + l3);
+    if (!active) return;
+    reinterpret_cast<int *>(q)[at] = pack4(l0, l1, l2, l3);
+    if (sub == 0) {
+        scales[g] = d;
+        corr[g] = -zp * sum;
+    }
+}
+
 // Prediction::greedy (lm.rs:169-179) over the head's per-workgroup candidates: the first index of
 // the largest logit; NaNs never win, and a NaN first logit keeps index 0.
 __global__ __launch_bounds__(1024) void greedy_kernel(const float *__restrict__ pval, const int32_t *__restrict__ pidx, int n,
@@ -530,6 +608,14 @@ struct fg_qwen2 {
     int chunks, per_chunk;
     size_t score_smem, weigh_smem, exact_smem;
     int zp;
+    // a prefill's rows (fg_qwen2_read), allocated on the first read and grown to its chunk
+    struct {
+        size_t rows;
+        float *x, *qkv, *gate, *up, *scores;  // [rows][hidden], [rows][qkv], [rows][ffn] x2, [rows][heads][capacity]
+        int8_t *lev;                          // [rows][widest]: the levels handed to the next product
+        float *lsc;                           // [rows][widest / 32]
+        int32_t *lco;
+    } pre;
 };
 
 namespace {
@@ -768,6 +854,141 @@ int head_launch(fg_qwen2 *m, hipStream_t st)
     return launch_proj(p, sh.dtype, IN_PREQ, OUT_STORE, sh.exact != 0, st);
 }
 
+// ------------------------------------------------------------------ prefill (Reader::read)
+
+void free_prefill(fg_qwen2 *m)
+{
+    void *ptrs[] = {m->pre.x, m->pre.qkv, m->pre.gate, m->pre.up, m->pre.scores, m->pre.lev, m->pre.lsc, m->pre.lco};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    m->pre = {};
+}
+
+// Room for `rows` rows of a prefill (grown once past what an earlier read used).
+int ensure_prefill(fg_qwen2 *m, size_t rows)
+{
+    if (m->pre.rows >= rows) return FG_OK;
+    free_prefill(m);
+    const fg_qwen2_shape &sh = m->shape;
+    const size_t qkv_w = (sh.heads + 2 * sh.kv_heads) * sh.head_dim, width = sh.heads * sh.head_dim;
+    const size_t widest = std::max(sh.hidden, std::max(width, sh.ffn));
+    struct {
+        void **ptr;
+        size_t bytes;
+    } allocs[] = {
+        {reinterpret_cast<void **>(&m->pre.x), rows * sh.hidden * 4},
+        {reinterpret_cast<void **>(&m->pre.qkv), rows * qkv_w * 4},
+        {reinterpret_cast<void **>(&m->pre.gate), rows * sh.ffn * 4},
+        {reinterpret_cast<void **>(&m->pre.up), rows * sh.ffn * 4},
+        {reinterpret_cast<void **>(&m->pre.scores), rows * sh.heads * sh.capacity * 4},
+        {reinterpret_cast<void **>(&m->pre.lev), rows * widest},
+        {reinterpret_cast<void **>(&m->pre.lsc), rows * widest / 32 * 4},
+        {reinterpret_cast<void **>(&m->pre.lco), rows * widest / 32 * 4},
+    };
+    for (auto &a : allocs) {
+        const hipError_t e = hipMalloc(a.ptr, a.bytes);
+        if (e != hipSuccess) {
+            free_prefill(m);
+            return check_hip(e, "fg_qwen2_read: hipMalloc");
+        }
+    }
+    m->pre.rows = rows;
+    return FG_OK;
+}
+
+// RMSNorm + quantize of the prefill's n rows (ops.rs:7-16, the model's order) into its levels.
+int prefill_norm(fg_qwen2 *m, const float *weight, int n, hipStream_t st)
+{
+    const fg_qwen2_shape &sh = m->shape;
+    ProjParams p{};
+    p.K = int(sh.hidden);
+    p.G = int(sh.hidden / 32);
+    p.B = p.G;
+    p.x = m->pre.x;
+    p.norm_w = weight;
+    p.eps = sh.eps;
+    p.zp = m->zp;
+    p.q_out = m->pre.lev;
+    p.s_out = m->pre.lsc;
+    p.c_out = m->pre.lco;
+    return launch_norm_quantize_rows(p, n, sh.exact != 0, st);
+}
+
+// The product of the prefill's n quantized rows (every output, the reference's group order) into
+// out (ld columns per row), written or added.
+int prefill_product(fg_qwen2 *m, const fg_table *t, int n, const float *bias, float *out, size_t ld, bool accumulate,
+                    hipStream_t st)
+{
+    ProductArgs a{};
+    a.t = t;
+    a.q = m->pre.lev;
+    a.as = m->pre.lsc;
+    a.corr = m->pre.lco;
+    a.rows = size_t(n);
+    a.quad_begin = 0;
+    a.quad_end = t->quads;
+    a.bias = bias;
+    a.out = out;
+    a.ld_out = ld;
+    a.accumulate = accumulate ? 1 : 0;
+    return launch_product(a, st);
+}
+
+// One layer over the prefill's n rows at positions first .. first + n - 1 (layer.rs:161-344 with
+// rows > 1): each step over every row, the products on the matrix cores.
+int prefill_layer(fg_qwen2 *m, size_t li, size_t first, int n, hipStream_t st)
+{
+    const fg_qwen2_shape &sh = m->shape;
+    const fg_qwen2_layer &ly = m->layers[li];
+    const size_t qkv_w = (sh.heads + 2 * sh.kv_heads) * sh.head_dim, width = sh.heads * sh.head_dim;
+    const size_t layer_base = li * sh.kv_heads * sh.capacity * sh.head_dim;
+    int rc;
+    // prepare + QKV (layer/input.rs:22-66), rotary embeddings and the kept keys and values
+    if ((rc = prefill_norm(m, ly.norm1, n, st))) return rc;
+    if ((rc = prefill_product(m, ly.qkv, n, ly.qkv_bias, m->pre.qkv, qkv_w, false, st))) return rc;
+    rope_keep_rows_kernel<<<dim3(unsigned(n), unsigned(sh.heads + 2 * sh.kv_heads)), unsigned(sh.head_dim / 2), 0, st>>>(
+        m->pre.qkv, qkv_w, m->rope, int(sh.heads), int(sh.kv_heads), int(sh.head_dim), m->kcache, m->vcache, layer_base,
+        int(sh.capacity), int(first));
+    FG_HIP(hipGetLastError());
+    // attention of every row over the keys up to its own position (Mask::Causal), its output row
+    // quantized for the output projection
+    AttnParams a{};
+    a.qkv = m->pre.qkv;
+    a.qkv_stride = qkv_w;
+    a.kcache = m->kcache;
+    a.vcache = m->vcache;
+    a.layer_base = layer_base;
+    a.heads = int(sh.heads);
+    a.kv_heads = int(sh.kv_heads);
+    a.D = int(sh.head_dim);
+    a.capacity = int(sh.capacity);
+    a.keys = int(first) + 1;
+    a.scores = m->pre.scores;
+    a.zp = m->zp;
+    a.q = m->pre.lev;
+    a.scales = m->pre.lsc;
+    a.corr = m->pre.lco;
+    a.row_width = width;
+    const dim3 sgrid(unsigned(sh.kv_heads), unsigned((first + n + kScoreKeys - 1) / kScoreKeys), unsigned(n));
+    attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
+    FG_HIP(hipGetLastError());
+    const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims), unsigned(n));
+    if (sh.exact) attn_weigh_kernel<true><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
+    else attn_weigh_kernel<false><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
+    FG_HIP(hipGetLastError());
+    // hidden += o(attention) (layer.rs:239-245)
+    if ((rc = prefill_product(m, ly.o, n, nullptr, m->pre.x, sh.hidden, true, st))) return rc;
+    // hidden += down(silu(gate(x))·up(x)), x the normed rows (layer.rs:249-344)
+    if ((rc = prefill_norm(m, ly.norm2, n, st))) return rc;
+    if ((rc = prefill_product(m, ly.gate, n, nullptr, m->pre.gate, sh.ffn, false, st))) return rc;
+    if ((rc = prefill_product(m, ly.up, n, nullptr, m->pre.up, sh.ffn, false, st))) return rc;
+    const size_t groups = size_t(n) * sh.ffn / 32;
+    swiglu_quantize_kernel<<<unsigned((groups * 8 + 255) / 256), 256, 0, st>>>(m->pre.gate, m->pre.up, groups, m->zp, m->pre.lev,
+                                                                              m->pre.lsc, m->pre.lco);
+    FG_HIP(hipGetLastError());
+    return prefill_product(m, ly.down, n, nullptr, m->pre.x, sh.hidden, true, st);
+}
+
 bool table_is(const fg_table *t, int dtype, size_t rows, size_t cols)
 {
     return t && t->dtype == dtype && t->rows == rows && t->cols == cols;
@@ -972,9 +1193,49 @@ extern "C" int fg_qwen2_step(fg_qwen2 *m, int token, size_t position, float *hid
     return FG_OK;
 }
 
+extern "C" int fg_qwen2_embed(fg_qwen2 *m, const int32_t *ids, size_t count, float *out, void *stream)
+{
+    if (!m || (count && (!ids || !out))) return set_error(FG_ERR_ARG, "fg_qwen2_embed: a null argument");
+    return launch_embed_rows(m->table, ids, count, out, as_stream(stream));
+}
+
+extern "C" int fg_qwen2_read(fg_qwen2 *m, const float *embeddings, size_t count, size_t first, size_t chunk, float *hidden,
+                             float *logits, int32_t *next_token, void *stream)
+{
+    if (!m || !embeddings) return set_error(FG_ERR_ARG, "fg_qwen2_read: a null argument");
+    const fg_qwen2_shape &sh = m->shape;
+    if (count == 0 || chunk == 0) return set_error(FG_ERR_SHAPE, "fg_qwen2_read: no rows, or chunks of none");
+    // transformer.rs:329-341: the cache holds every key the span sees
+    if (first + count > sh.capacity) return set_error(FG_ERR_SHAPE, "fg_qwen2_read: the cache holds every key the span sees");
+    chunk = std::min(std::min(chunk, count), size_t(4096));
+    hipStream_t st = as_stream(stream);
+    int rc = ensure_prefill(m, chunk);
+    if (rc) return rc;
+    for (size_t start = 0; start < count; start += chunk) {
+        const size_t n = std::min(chunk, count - start);
+        FG_HIP(hipMemcpyAsync(m->pre.x, embeddings + start * sh.hidden, n * sh.hidden * 4, hipMemcpyDeviceToDevice, st));
+        for (size_t l = 0; l < sh.layers; l++)
+            if ((rc = prefill_layer(m, l, first + start, int(n), st))) return rc;
+        if (start + n == count)
+            FG_HIP(hipMemcpyAsync(m->hidden, m->pre.x + (n - 1) * sh.hidden, sh.hidden * 4, hipMemcpyDeviceToDevice, st));
+    }
+    // the last row's prediction (Prediction::predict, lm.rs:147-166)
+    if (hidden) FG_HIP(hipMemcpyAsync(hidden, m->hidden, sh.hidden * 4, hipMemcpyDeviceToDevice, st));
+    if (logits || next_token) {
+        if ((rc = head_launch(m, st))) return rc;
+        if (logits) FG_HIP(hipMemcpyAsync(logits, m->logits, sh.vocab * 4, hipMemcpyDeviceToDevice, st));
+        if (next_token) {
+            greedy_kernel<<<1, 1024, 0, st>>>(m->pval, m->pidx, m->head_groups, m->logits, next_token);
+            FG_HIP(hipGetLastError());
+        }
+    }
+    return FG_OK;
+}
+
 extern "C" int fg_qwen2_free(fg_qwen2 *m)
 {
     if (!m) return FG_OK;
+    free_prefill(m);
     void *ptrs[] = {m->hidden, m->qkv, m->logits, m->rope, m->xq, m->xs, m->xc, m->pval, m->pidx, m->scores, m->part};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);

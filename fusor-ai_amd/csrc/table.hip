@@ -287,6 +287,37 @@ int launch_encode(int dtype, size_t rows, size_t cols, const float *values, uint
     return FG_OK;
 }
 
+// Lm::embed (lm.rs:97-108): row ids[y] of the table into out[y], one thread per value. An id past
+// the table's rows (where the reference's slice index panics) reads nothing and gives a row of NaN.
+__global__ void embed_rows_kernel(const int8_t *__restrict__ codes, const float *__restrict__ scales, int dtype,
+                                  const int32_t *__restrict__ ids, size_t rows, size_t cols, float *__restrict__ out)
+{
+    const size_t k = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= cols) return;
+    const size_t row = size_t(uint32_t(ids[blockIdx.y]));
+    if (row >= rows) {
+        out[size_t(blockIdx.y) * cols + k] = __builtin_nanf("");
+        return;
+    }
+    const int group = dtype == FG_T2B128 ? 128 : 32;
+    const size_t blocks = cols / 32, groups = cols / group, quad = row / 4, b = k / 32;
+    const int lane = int(row % 4);
+    const int qbytes = dtype == FG_Q4B32 ? 64 : dtype == FG_T2B128 ? 32 : 128;
+    const int level = device_level(dtype, codes + (quad * blocks + b) * qbytes, lane, int(k % 32));
+    const float scale = scales[(quad * groups + b / (group / 32)) * 4 + lane];
+    out[size_t(blockIdx.y) * cols + k] = scale * float(level);
+}
+
+int launch_embed_rows(const fg_table *t, const int32_t *ids, size_t count, float *out, hipStream_t s)
+{
+    if (t->cols == 0 || count == 0) return FG_OK;
+    if (count > 65535) return set_error(FG_ERR_SHAPE, "at most 65535 rows per embedding call");
+    embed_rows_kernel<<<dim3(unsigned((t->cols + 255) / 256), unsigned(count)), 256, 0, s>>>(t->codes, t->scales, t->dtype, ids,
+                                                                                             t->rows, t->cols, out);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
+}
+
 int launch_dequantize_row(const fg_table *t, size_t row, float *out, hipStream_t s)
 {
     if (t->cols == 0) return FG_OK;

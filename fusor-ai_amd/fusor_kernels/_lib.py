@@ -80,6 +80,8 @@ SIGNATURES = {
     "fg_qwen2_layer_forward": (_I, [_P, _S, _S, _P, _P]),
     "fg_qwen2_attention": (_I, [_P, _S, _S, _P, _P, _P, _P]),
     "fg_qwen2_layer_probe": (_I, [_P, _S, _S, _P, ctypes.POINTER(FgQwen2Probe), _P]),
+    "fg_qwen2_embed": (_I, [_P, _P, _S, _P, _P]),
+    "fg_qwen2_read": (_I, [_P, _P, _S, _S, _S, _P, _P, _P, _P]),
     "fg_qwen2_free": (_I, [_P]),
 }
 

@@ -60,6 +60,22 @@ class Qwen2:
         check(lib().fg_qwen2_step(self.handle, int(token), int(position), ptr(hidden), ptr(logits), ptr(next_token),
                                   stream_handle(stream)))
 
+    def embed(self, ids, out=None, stream=None):
+        """Lm::embed (lm.rs:97-108): the table's rows of the device int32 token ids, [count, hidden]."""
+        import torch
+        if out is None:
+            out = torch.empty((ids.numel(), self.shape.hidden), dtype=torch.float32, device=ids.device)
+        check(lib().fg_qwen2_embed(self.handle, ptr(ids), ids.numel(), ptr(out), stream_handle(stream)))
+        return out
+
+    def read(self, embeddings, first, chunk, hidden=None, logits=None, next_token=None, stream=None):
+        """Reader::read (lm.rs:205-228): the device rows `embeddings` [count, hidden] from position
+        `first`, `chunk` rows per call of the stack; the last row's residual row, logits and greedy
+        token into the given device tensors."""
+        count = embeddings.numel() // self.shape.hidden
+        check(lib().fg_qwen2_read(self.handle, ptr(embeddings), count, int(first), int(chunk), ptr(hidden), ptr(logits),
+                                  ptr(next_token), stream_handle(stream)))
+
     def layer_forward(self, layer, position, hidden, stream=None):
         check(lib().fg_qwen2_layer_forward(self.handle, layer, position, ptr(hidden), stream_handle(stream)))
 

@@ -272,6 +272,22 @@ typedef struct {
  * the caches, `hidden` is not changed. */
 int fg_qwen2_layer_probe(fg_qwen2 *model, size_t layer, size_t position, const float *hidden,
                          const fg_qwen2_probe *probe, void *stream);
+/* Lm::embed (blocks/src/lm.rs:97-108): the tied table's rows of the device token ids `ids`
+ * (count of them) into device `out` [count][hidden]. */
+int fg_qwen2_embed(fg_qwen2 *model, const int32_t *ids, size_t count, float *out, void *stream);
+/* Reader::read (blocks/src/lm.rs:205-228) with sequential positions: `count` device rows of
+ * `embeddings` [count][hidden] read from position `first` (the cache already holds the positions
+ * before it), `chunk` rows per call of the stack (Transformer::forward with rows > 1,
+ * transformer.rs:294-341, Mask::Causal): per layer every row is normed and quantized, its
+ * products run on the matrix cores over all the chunk's rows, each row attends to the keys up to its
+ * own position, and the keys and values of every row are kept. Then the last row's prediction
+ * (Prediction::predict, lm.rs:147-166). Outputs (device, any may be NULL): hidden [hidden] (the last
+ * row's residual stream), logits [vocab], next_token [1]. first + count must not pass the cache's
+ * capacity (transformer.rs:329-341). The model's order applies: exact, the reference's reductions,
+ * bit-identical to one decode step per row; else the parallel ones. The first read allocates the
+ * rows' buffers (for min(chunk, count, 4096) rows; a larger chunk later grows them). */
+int fg_qwen2_read(fg_qwen2 *model, const float *embeddings, size_t count, size_t first, size_t chunk, float *hidden,
+                  float *logits, int32_t *next_token, void *stream);
 int fg_qwen2_free(fg_qwen2 *model);
 
 #ifdef __cplusplus

@@ -862,3 +862,53 @@ int or_qwen2_step(const or_qwen2_shape *sh, const or_qwen2_layer *layers, const 
     free(sin_v);
     return 0;
 }
+
+/* lm.rs:97-108 */
+void or_qwen2_embed(const or_qwen2_shape *sh, const uint8_t *table, const int *ids, size_t count, float *out)
+{
+    for (size_t r = 0; r < count; r++) or_dequantize_row(sh->dtype, sh->vocab, sh->hidden, table, (size_t)ids[r], out + r * sh->hidden);
+}
+
+/* Reader::read (lm.rs:205-228): chunks of rows through the stack, each layer over every row of the
+ * chunk before the next layer (Stack::forward_layers). Within a layer the reference projects every
+ * row, keeps their keys and values, then attends each row over the keys up to its own position
+ * (Mask::Causal, transformer.rs:185-219): row r reads only rows 0..r of the chunk, all kept by then,
+ * so taking the rows one after another through or_qwen2_layer_forward is that arithmetic. */
+int or_qwen2_read(const or_qwen2_shape *sh, const or_qwen2_layer *layers, const float *final_norm,
+                  const uint8_t *table, float *kcache, float *vcache, const float *embeddings, size_t count,
+                  size_t first, size_t chunk, float *hidden_out, float *logits, int *next_token, int threads)
+{
+    size_t H = sh->hidden, half = sh->head_dim / 2;
+    if (count == 0 || chunk == 0) return -1;
+    if (first + count > sh->capacity) return -1; /* transformer.rs:329-341 */
+    float *rows = (float *)malloc(chunk * H * sizeof(float));
+    float *inv = (float *)malloc(half * sizeof(float));
+    float *cos_v = (float *)malloc(chunk * half * sizeof(float));
+    float *sin_v = (float *)malloc(chunk * half * sizeof(float));
+    or_rope_inv_freq(sh->rope_base, sh->head_dim, inv);
+    for (size_t start = 0; start < count; start += chunk) {
+        size_t n = count - start < chunk ? count - start : chunk;
+        memcpy(rows, embeddings + start * H, n * H * sizeof(float));
+        for (size_t r = 0; r < n; r++) or_rope_angles(inv, half, first + start + r, cos_v + r * half, sin_v + r * half);
+        for (size_t l = 0; l < sh->layers; l++)
+            for (size_t r = 0; r < n; r++)
+                or_qwen2_layer_forward(sh, &layers[l], l, kcache, vcache, first + start + r, cos_v + r * half,
+                                       sin_v + r * half, rows + r * H, threads);
+        if (start + n == count) {
+            const float *last = rows + (n - 1) * H;
+            if (hidden_out) memcpy(hidden_out, last, H * sizeof(float));
+            if (logits) { /* Prediction::predict (lm.rs:147-166) of the last row */
+                float *normed = (float *)malloc(H * sizeof(float));
+                or_rms_norm(last, final_norm, H, sh->eps, normed);
+                project_row(sh, table, sh->vocab, H, normed, NULL, logits, threads);
+                if (next_token) *next_token = or_greedy(logits, sh->vocab);
+                free(normed);
+            }
+        }
+    }
+    free(rows);
+    free(inv);
+    free(cos_v);
+    free(sin_v);
+    return 0;
+}

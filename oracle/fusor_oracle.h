@@ -167,6 +167,17 @@ int or_qwen2_step(const or_qwen2_shape *shape, const or_qwen2_layer *layers,
                   int token, size_t position, float *hidden_out, float *logits, int *next_token,
                   int threads);
 int or_greedy(const float *logits, size_t n); /* lm.rs:169-179 */
+/* Lm::embed (lm.rs:97-108): the table's rows of `ids`, count x hidden, into `out`. */
+void or_qwen2_embed(const or_qwen2_shape *shape, const uint8_t *table, const int *ids, size_t count, float *out);
+/* Reader::read (lm.rs:205-228) with sequential positions: `count` rows of embeddings (count x
+ * hidden) from position `first`, `chunk` rows per call of the stack, each call running every layer
+ * over its rows (transformer.rs:294-341, Mask::Causal); then for the last row the final norm, the
+ * logits and the greedy token (Prediction::predict, lm.rs:147-166). hidden_out (the last row's
+ * residual stream), logits and next_token may be NULL. Returns -1 when the cache does not hold
+ * every key the rows see (transformer.rs:329-341). */
+int or_qwen2_read(const or_qwen2_shape *shape, const or_qwen2_layer *layers, const float *final_norm,
+                  const uint8_t *table, float *kcache, float *vcache, const float *embeddings, size_t count,
+                  size_t first, size_t chunk, float *hidden_out, float *logits, int *next_token, int threads);
 
 /* One int8 attention call (blocks/src/attention.rs:35-47): head h of row r of an operand is the
  * head_dim values at r * stride + offset + h * head_dim; `images` images of `queries` query rows

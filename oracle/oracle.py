@@ -92,6 +92,8 @@ def _declare(l):
         "or_rng_fill_normal": (None, [_P, _P, _S]),
         "or_qwen2_layer_forward": (_I, [_P, _P, _S, _P, _P, _S, _P, _P, _P, _I]),
         "or_qwen2_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _S, _P, _P, _P, _I]),
+        "or_qwen2_embed": (None, [_P, _P, _P, _S, _P]),
+        "or_qwen2_read": (_I, [_P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _P, _P, _P, _I]),
         "or_greedy": (_I, [_P, _S]),
     }
     for name, (res, args) in sig.items():
@@ -360,3 +362,25 @@ class Qwen2:
                                      _ptr(kcache), _ptr(vcache), position, _ptr(cos), _ptr(sin),
                                      _ptr(hidden), threads)
         return hidden
+
+    def embed(self, ids):
+        """Lm::embed (lm.rs:97-108): the table's rows of `ids`."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.zeros((ids.size, self.shape.hidden), np.float32)
+        lib().or_qwen2_embed(ctypes.byref(self.shape), _ptr(self.table), _ptr(ids), ids.size, _ptr(out))
+        return out
+
+    def read(self, kcache, vcache, embeddings, first, chunk, threads=1, logits=True):
+        """Reader::read (lm.rs:205-228): the rows of `embeddings` from position `first`, `chunk` rows
+        per call of the stack; returns the last row's hidden state, logits and greedy token."""
+        sh = self.shape
+        emb = np.ascontiguousarray(embeddings, dtype=np.float32).reshape(-1, sh.hidden)
+        hidden = np.zeros(sh.hidden, np.float32)
+        out = np.zeros(sh.vocab, np.float32) if logits else None
+        nxt = ctypes.c_int(-1)
+        rc = lib().or_qwen2_read(ctypes.byref(sh), ctypes.cast(self.layers, ctypes.c_void_p), _ptr(self.final_norm),
+                                 _ptr(self.table), _ptr(kcache), _ptr(vcache), _ptr(emb), emb.shape[0], first, chunk,
+                                 _ptr(hidden), _ptr(out), ctypes.byref(nxt), threads)
+        if rc != 0:
+            raise ValueError("the cache holds every key the span sees")
+        return hidden, out, nxt.value

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from gpu_data import synthetic_table
+from gpu_data import qwen2_model as build
 
 pytestmark = pytest.mark.gpu
 
@@ -40,32 +40,6 @@ def rel_l2(got, want):
     got = got.astype(np.float64)
     want = want.astype(np.float64)
     return float(np.sqrt(np.sum((got - want) ** 2) / np.sum(want * want)))
-
-
-def build(dtype, hidden, layers, heads, kv_heads, head_dim, ffn, vocab, capacity, seed, synthetic):
-    rng = np.random.default_rng(seed)
-    qkv_w = (heads + 2 * kv_heads) * head_dim
-    lys = []
-    for li in range(layers):
-        f = {}
-        for j, (name, (r, c)) in enumerate({"qkv": (qkv_w, hidden), "o": (hidden, heads * head_dim), "gate": (ffn, hidden),
-                                            "up": (ffn, hidden), "down": (hidden, ffn)}.items()):
-            if synthetic:
-                f[name] = synthetic_table(dtype, r, c, seed=seed * 1000 + li * 10 + j)
-            else:
-                f[name] = O.encode(dtype, r, c, (rng.standard_normal((r, c)) / math.sqrt(c)).astype(np.float32))
-        f["norm1"] = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
-        f["norm2"] = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
-        f["qkv_bias"] = (0.1 * rng.standard_normal(qkv_w)).astype(np.float32)
-        lys.append(f)
-    final = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
-    table = synthetic_table(dtype, vocab, hidden, seed=seed + 7) if synthetic else \
-        O.encode(dtype, vocab, hidden, rng.standard_normal((vocab, hidden)).astype(np.float32))
-    kc = rng.standard_normal((layers, kv_heads, capacity, head_dim)).astype(np.float32)
-    vc = rng.standard_normal((layers, kv_heads, capacity, head_dim)).astype(np.float32)
-    sh = O.Qwen2Shape(hidden=hidden, layers=layers, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=ffn,
-                      vocab=vocab, capacity=capacity, rope_base=1e6, eps=1e-6, dtype=dtype)
-    return sh, lys, final, table, kc, vc
 
 
 def gpu_model(fk, dtype, sh, lys, final, table, kc, vc, exact):

@@ -198,36 +198,76 @@ def matvec_bytes(n, k, dtype=Q7B32, residual=False, f32_input=False):
     return codes + scales + act + out
 
 
-def build_decoder(fk, torch, np, exact, seed=0):
+def build_decoder(fk, torch, np, exact, seed=0, dtype=Q7B32):
     shape = fk.Shape()
     rng = np.random.default_rng(seed)
     H, F, V = shape.hidden, shape.ffn, shape.vocab
     dims = {"qkv": (shape.qkv(), H), "o": (H, shape.width()), "gate": (F, H), "up": (F, H), "down": (H, F)}
     layers = []
     for _ in range(shape.layers):
-        d = {k: fk.Table(fk.Tensor(Q7B32, list(v), synthetic_table(np, Q7B32, v[0], v[1], rng))) for k, v in dims.items()}
+        d = {k: fk.Table(fk.Tensor(dtype, list(v), synthetic_table(np, dtype, v[0], v[1], rng))) for k, v in dims.items()}
         d["norm1"] = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
         d["norm2"] = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
         d["qkv_bias"] = torch.from_numpy((0.1 * rng.standard_normal(shape.qkv())).astype(np.float32)).cuda()
         layers.append(d)
-    table_bytes = synthetic_table(np, Q7B32, V, H, rng)
-    head = fk.Table(fk.Tensor(Q7B32, [V, H], table_bytes))
+    table_bytes = synthetic_table(np, dtype, V, H, rng)
+    head = fk.Table(fk.Tensor(dtype, [V, H], table_bytes))
     final = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
     cache_shape = (shape.layers, shape.kv_heads, shape.capacity, shape.head_dim)
     kc = torch.from_numpy(rng.standard_normal(cache_shape).astype(np.float32)).cuda()
     vc = torch.from_numpy(rng.standard_normal(cache_shape).astype(np.float32)).cuda()
-    model = fk.Qwen2(shape, Q7B32, layers, final, head, kc, vc, exact=exact)
+    model = fk.Qwen2(shape, dtype, layers, final, head, kc, vc, exact=exact)
     host = {"layers": layers, "head": head, "final": final, "table_bytes": table_bytes, "kc": kc, "vc": vc}
     return shape, model, host
 
 
-def decode_step_bytes(shape, position):
+def decode_step_bytes(shape, position, dtype=Q7B32):
     """Algorithmic bytes of one decode step (weights, KV read, activations)."""
     H, F, D = shape.hidden, shape.ffn, shape.head_dim
-    per_layer = (matvec_bytes(shape.qkv(), H) + shape.qkv() * 4 + matvec_bytes(H, shape.width(), residual=True)
-                 + 2 * matvec_bytes(F, H) + matvec_bytes(H, F, residual=True))
+    per_layer = (matvec_bytes(shape.qkv(), H, dtype) + shape.qkv() * 4 + matvec_bytes(H, shape.width(), dtype, residual=True)
+                 + 2 * matvec_bytes(F, H, dtype) + matvec_bytes(H, F, dtype, residual=True))
     kv = 2 * (position + 1) * shape.kv_heads * D * 4
-    return shape.layers * (per_layer + kv) + matvec_bytes(shape.vocab, H)
+    return shape.layers * (per_layer + kv) + matvec_bytes(shape.vocab, H, dtype)
+
+
+def time_prefill(fk, torch, np, model, shape, rows, chunk, reps=10):
+    """Reader::read of `rows` token rows from position 0 (embedding included), as one HIP graph."""
+    ids = torch.from_numpy(np.random.default_rng(7).integers(0, shape.vocab, rows).astype(np.int32)).cuda()
+    emb = torch.empty((rows, shape.hidden), dtype=torch.float32, device="cuda")
+    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def read():
+        model.embed(ids, out=emb)
+        model.read(emb, 0, chunk, next_token=nxt)
+    ms = Timer(torch)(read, reps, warmup=2, graph=True)
+    return {"rows": rows, "chunk": chunk, "ms": round(ms, 4), "rows_per_s": round(rows / ms * 1e3, 1)}
+
+
+def cpu_prefill_baseline(np, shape, host, rows):
+    """The oracle's Reader::read of `rows` rows from position 0 (the reference's scalar path, its
+    products column-split over a team of threads), one warm-up then the mean of two reads."""
+    from oracle import oracle as O
+    layers = []
+    for d in host["layers"]:
+        layers.append({k: d[k].reference_bytes() for k in ("qkv", "o", "gate", "up", "down")}
+                      | {k: d[k].cpu().numpy() for k in ("norm1", "norm2", "qkv_bias")})
+    sh = O.Qwen2Shape(hidden=shape.hidden, layers=shape.layers, heads=shape.heads, kv_heads=shape.kv_heads,
+                      head_dim=shape.head_dim, ffn=shape.ffn, vocab=shape.vocab, capacity=shape.capacity,
+                      rope_base=shape.rope_base, eps=shape.eps, dtype=O.Q7B32)
+    model = O.Qwen2(sh, layers, host["final"].cpu().numpy(), host["table_bytes"])
+    kc, vc = host["kc"].cpu().numpy(), host["vc"].cpu().numpy()
+    emb = model.embed(np.random.default_rng(7).integers(0, shape.vocab, rows).astype(np.int32))
+    default, _ = cpu_thread_counts()
+    cpu_model, nproc, _ = host_cpu()
+    call = lambda: model.read(kc, vc, emb, 0, rows, threads=default)  # noqa: E731
+    call()
+    t0 = time.perf_counter()
+    for _ in range(2):
+        call()
+    ms = (time.perf_counter() - t0) * 1e3 / 2
+    return {"value": round(rows / ms * 1e3, 2), "unit": "rows/s", "ms": round(ms, 1), "cores": default, "kind": "port",
+            "cpu": cpu_model, "nproc": nproc,
+            "sample": f"a {rows}-row read from position 0 with the last row's logits, one warm-up then the mean of two"}
 
 
 def time_decode(fk, torch, model, position, steps, warmup):
@@ -586,7 +626,20 @@ def main():
         ex_model = fk.Qwen2(shape, Q7B32, host["layers"], host["final"], host["head"], host["kc"], host["vc"], exact=True)
         ms_x, _, _ = time_decode(fk, torch, ex_model, position, max(20, args.steps // 4), 5)
         other["exact_order_decode"] = {"ms_per_step": round(ms_x, 4), "tokens_per_s": round(1000.0 / ms_x, 1)}
+        # prefill (Reader::read) of 158 rows, the reference's prefill length, in one chunk: the
+        # parallel-order model and the exact one (bit-identical to one decode step per row)
+        other["prefill_158_rows"] = time_prefill(fk, torch, np, model, shape, 158, 158)
+        other["prefill_158_rows"]["exact_order"] = time_prefill(fk, torch, np, ex_model, shape, 158, 158)
+        if not args.no_cpu:
+            other["prefill_158_rows"]["cpu_baseline"] = cpu_prefill_baseline(np, shape, host, 32)
         del ex_model
+        # the same step with Q4b32 tables (the reference's LM layers run Q4b32), parallel order
+        _, q4_model, q4_host = build_decoder(fk, torch, np, exact=False, seed=1, dtype=Q4B32)
+        ms_4, _, _ = time_decode(fk, torch, q4_model, position, max(20, args.steps // 4), 5)
+        b4 = decode_step_bytes(shape, position, Q4B32)
+        other["q4b32_decode"] = {"ms_per_step": round(ms_4, 4), "tokens_per_s": round(1000.0 / ms_4, 1),
+                                 "step_bytes": b4, "step_GB_s": round(b4 / ms_4 / 1e6, 1)}
+        del q4_model, q4_host
     if not args.no_extras:
         log("extra workloads...")
         other.update(extras(fk, torch, np, with_cpu=not args.no_cpu))

@@ -99,3 +99,30 @@ def test_tile_scale_products_below_the_normal_range(fk, monkeypatch, tile, dtype
     got = host(fk.matmul(t.matrix(), fk.Input(f32=dev(x.reshape(-1))), range(0, 72)))
     assert same_bits(got, want), first_mismatch(got, want)
     assert np.all(np.isfinite(want)) and np.any(want != 0)
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+@pytest.mark.parametrize("rows,n,k", [(17, 96, 2048), (64, 260, 4864), (158, 896, 2048), (256, 132, 3072)])
+def test_row_bands_over_a_long_k(fk, dtype, rows, n, k):
+    """17 to 256 rows over 64 or more blocks take the paired 16-row tiles in bands of 16 rows: a last
+    band that ends inside its tile, a last column tile of two quads, f32 and pre-quantized rows, a
+    column range starting inside the table with bias, added to a residual."""
+    print(f"row bands dtype {dtype} {rows}x{k}->{n}", flush=True)
+    data = synthetic_table(dtype, n, k, seed=rows + n + k + 1)
+    t = fk.Table(fk.Tensor(dtype, [n, k], data))
+    m = t.matrix()
+    x = activations(rows, k, seed=rows + k, outliers=0.01)
+    width = (n + 3) // 4 * 4
+    want = oracle(dtype, n, k, data, x, rows)
+    got = host(fk.matmul(m, fk.Input(f32=dev(x.reshape(-1))), range(0, width)))
+    assert same_bits(got, want), first_mismatch(got, want)
+    inp = fk.QuantizedRows().input(m, dev(x.reshape(-1)))
+    got = host(fk.matmul(m, inp, range(0, width)))
+    assert same_bits(got, want), first_mismatch(got, want)
+    bias = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    lo, hi = 4, width
+    h0 = np.random.default_rng(k).standard_normal((rows, hi - lo)).astype(np.float32)
+    h = dev(h0)
+    fk.matmul(m, inp, range(lo, hi), bias=dev(bias), out=h, accumulate=True)
+    want_b = oracle(dtype, n, k, data, x, rows, lo, hi, bias=bias)
+    assert same_bits(host(h), (h0 + want_b).astype(np.float32))

@@ -20,6 +20,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace fg {
@@ -988,6 +989,148 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(GemmParams p)
         }
 }
 
+// Few 32 x 32 output tiles (512 x 4864 -> 896: 448 tiles for 1024 SIMDs) under the fused scaling: a
+// workgroup of four waves owns one 32 x 32 tile and wave w its 16 x 16 quarter (w / 2, w % 2) over
+// every block in group order with v_mfma_i32_16x16x32_i8 (K = one block), so no wave hands a term to
+// another and no barrier waits on a term. The tile's operands for kQuarterBlocks blocks at a time (a
+// stage) arrive by direct global-to-LDS loads, DEPTH stages in flight, and each wave reads its 16
+// rows and 16 columns from them:
+//   A  [kb][32 rows][32 B]  activation levels (q [M][K], row-major);
+//   W  [kb][32 cols][32 B]  weight levels (Q8; Q4: [kb][32 cols][16 B] packed nibbles);
+//   AS [kb][32 rows]        activation scales, from the rows' [M][G] scales by 4-byte loads;
+//   WS [kb][32 cols]        weight scales, the table's ((q·G + g)·4 + lane) order per quad.
+// Operands (16x16x32): lane l feeds row (or column) l % 16 with inputs 8·(l / 16) .. + 7 of the
+// block; the product of lane l is column l % 16, rows 4·(l / 16) + v. The scale products of four
+// blocks come from one f32 outer product (v_mfma_f32_16x16x1_4b_f32) in the same layout, exactly
+// the VALU's rounded fl(ws·as). Rows and columns past the edges re-read the last valid one; blocks
+// past the last are loaded clamped and skipped.
+constexpr int kQuarterBlocks = 8;
+
+template <int FMT>
+struct QuarterTile {
+    static constexpr int KB = kQuarterBlocks;
+    static constexpr int RB = FMT == 8 ? 32 : 16;  // weight bytes of a column and block
+    static constexpr int A_BYTES = KB * 32 * 32, W_BYTES = KB * 32 * RB, AS_BYTES = KB * 32 * 4, WS_BYTES = KB * 32 * 4;
+    static constexpr int STAGE = A_BYTES + W_BYTES + AS_BYTES + WS_BYTES;
+    // each wave's direct loads of a stage: A, W (1 KiB each), AS (4 bytes a lane), WS (16 lanes)
+    static constexpr int A_LOADS = KB / 4, W_LOADS = KB * RB / 32 / 4;
+    static constexpr int LOADS = A_LOADS + W_LOADS + 2;
+    static_assert(KB % 4 == 0 && A_LOADS >= 1 && W_LOADS >= 1 && KB * 32 * 4 == 4 * 256, "quarter stage shape");
+};
+
+template <int FMT, int DEPTH, bool FUSED>
+__global__ __launch_bounds__(256) void gemm_quarter_kernel(GemmParams p)
+{
+    using T = QuarterTile<FMT>;
+    constexpr int KB = T::KB, QB = FMT == 8 ? 128 : 64, kALoads = T::A_LOADS, kWLoads = T::W_LOADS, kLoads = T::LOADS;
+    constexpr int kStage = T::STAGE, kA = T::A_BYTES, kW = T::W_BYTES, kAS = T::AS_BYTES;
+    extern __shared__ __align__(16) unsigned char quarter_lds[];  // [DEPTH][STAGE]
+    const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, s = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int tx, ty;
+    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 31) / 32, (p.M + 31) / 32, tx, ty);
+    const int m0 = ty * 32, n0 = p.col_begin + tx * 32;
+    const int B = p.B, G = p.G, K = p.K, last_col = p.col_end - 1;
+    const int stages = (B + KB - 1) / KB;
+
+    auto issue = [&](int st, int buf) {
+        unsigned char *base = quarter_lds + buf * kStage;
+        const int b0 = st * KB;
+#pragma unroll
+        for (int j = 0; j < kALoads; j++) {  // block kb; lane l: row l / 2, half l % 2
+            const int kb = wave * kALoads + j;
+            const int row = min(m0 + (lane >> 1), p.M - 1), blk = min(b0 + kb, B - 1);
+            __builtin_amdgcn_global_load_lds(p.q + size_t(row) * K + blk * 32 + (lane & 1) * 16, base + kb * 1024, 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < kWLoads; j++) {  // 1 KiB piece k of the stage's weight levels
+            const int k = wave * kWLoads + j;
+            const int8_t *src;
+            if (FMT == 8) {  // block k; lane l: column l / 2, half l % 2
+                const int col = min(n0 + (lane >> 1), last_col), blk = min(b0 + k, B - 1);
+                src = p.codes + size_t(col >> 2) * B * QB + size_t(blk) * QB + (col & 3) * 32 + (lane & 1) * 16;
+            } else {  // blocks 2k + l / 32; lane l: column l % 32
+                const int col = min(n0 + (lane & 31), last_col), blk = min(b0 + 2 * k + (lane >> 5), B - 1);
+                src = p.codes + size_t(col >> 2) * B * QB + size_t(blk) * QB + (col & 3) * 16;
+            }
+            __builtin_amdgcn_global_load_lds(src, base + kA + k * 1024, 16, 0, 0);
+        }
+        {  // AS position 64·wave + lane: block pos / 32, row pos % 32
+            const int pos = 64 * wave + lane;
+            const int row = min(m0 + (pos & 31), p.M - 1), blk = min(b0 + (pos >> 5), B - 1);
+            __builtin_amdgcn_global_load_lds(p.as + size_t(row) * G + blk, base + kA + kW + wave * 256, 4, 0, 0);
+        }
+        if (lane < 16) {  // WS: blocks 2·wave + l / 8, quad l % 8 (its four columns' scales)
+            const int q = min((n0 >> 2) + (lane & 7), last_col >> 2), blk = min(b0 + 2 * wave + (lane >> 3), B - 1);
+            __builtin_amdgcn_global_load_lds(p.wscales + (size_t(q) * G + blk) * 4, base + kA + kW + kAS + wave * 256, 16, 0, 0);
+        }
+    };
+
+    const int wr = 16 * (wave >> 1), wc = 16 * (wave & 1);
+    const int a_off = (wr + c) * 32 + 8 * s;
+    const int w_off = kA + (FMT == 8 ? (wc + c) * 32 + 8 * s : (wc + c) * 16 + 8 * (s & 1));
+    const int shift = FMT == 8 ? 0 : 4 * (s >> 1);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // the blocks [0, live) of the stage in `base`, in order (CHECK: live < KB, the last stage)
+    auto compute = [&](const unsigned char *base, int live, auto check) {
+        constexpr bool CHECK = decltype(check)::value;
+#pragma unroll
+        for (int j4 = 0; j4 < KB / 4; j4++) {
+            const float as = *reinterpret_cast<const float *>(base + kA + kW + ((4 * j4 + s) * 32 + wr + c) * 4);
+            const float ws = *reinterpret_cast<const float *>(base + kA + kW + kAS + ((4 * j4 + s) * 32 + wc + c) * 4);
+            long a[4], w[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int kb = 4 * j4 + b;
+                a[b] = *reinterpret_cast<const long *>(base + kb * 1024 + a_off);
+                w[b] = *reinterpret_cast<const long *>(base + kb * (32 * T::RB) + w_off);
+            }
+            const v16f zero16 = {0};
+            const v16f pp = __builtin_amdgcn_mfma_f32_16x16x1f32(as, ws, zero16, 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (CHECK && 4 * j4 + b >= live) break;  // uniform
+                long x = w[b];
+                if (FMT == 4) {
+                    const int lo = nibbles_signed(int(x) >> shift), hi = nibbles_signed(int(x >> 32) >> shift);
+                    x = long(unsigned(lo)) | (long(hi) << 32);
+                }
+                const v4i zero = {0, 0, 0, 0};
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[b], x, zero, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[v] = FUSED ? __builtin_fmaf(float(d[v]), pp[4 * b + v], acc[v]) : acc[v] + float(d[v]) * pp[4 * b + v];
+            }
+        }
+    };
+
+#pragma unroll
+    for (int k = 0; k < DEPTH - 1; k++)
+        if (k < stages) issue(k, k);
+    for (int st = 0; st < stages; st++) {
+        // this wave's loads of stage st (the later stages issued may still be in flight)
+        if (st + DEPTH - 2 < stages) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((DEPTH - 2) * kLoads) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // every wave's loads of stage st; every wave done reading the buffer refilled next
+        stage_barrier();
+        if (st + DEPTH - 1 < stages) issue(st + DEPTH - 1, (st + DEPTH - 1) % DEPTH);
+        const unsigned char *base = quarter_lds + (st % DEPTH) * kStage;
+        if (st + 1 < stages) compute(base, KB, std::false_type{});
+        else compute(base, B - st * KB, std::true_type{});
+    }
+    const int n = n0 + wc + c;
+    if (n > last_col) return;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int r = m0 + wr + 4 * s + v;
+        if (r >= p.M) continue;
+        float *o = p.out + size_t(r) * p.ld_out + (n - p.col_begin);
+        float y = acc[v];
+        if (p.bias && n < p.n_rows) y = y + p.bias[n];
+        *o = p.accumulate ? *o + y : y;
+    }
+}
+
 // as [M][G] -> as_t [G][Mpad] (zeros past M).
 __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int G, int Mpad, float *__restrict__ as_t)
 {
@@ -995,6 +1138,20 @@ __global__ void transpose_scales_kernel(const float *__restrict__ as, int M, int
     if (id >= size_t(G) * Mpad) return;
     const int g = int(id / Mpad), r = int(id % Mpad);
     as_t[id] = r < M ? as[size_t(r) * G + g] : 0.0f;
+}
+
+// One workgroup per 32 x 32 tile, four waves on its 16 x 16 quarters (gemm_quarter_kernel).
+template <int FMT, int DEPTH, bool FUSED>
+int launch_quarter(const GemmParams &p, hipStream_t s)
+{
+    const long tiles = long((p.col_end - p.col_begin + 31) / 32) * ((p.M + 31) / 32);
+    const size_t smem = size_t(DEPTH) * QuarterTile<FMT>::STAGE;
+    if (smem > 64 * 1024)
+        FG_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_quarter_kernel<FMT, DEPTH, FUSED>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    gemm_quarter_kernel<FMT, DEPTH, FUSED><<<unsigned(tiles), 256, smem, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
 }
 
 // 32 x 64 tiles per wave where they still give every SIMD a wave or more, else 32 x 32.
@@ -1041,6 +1198,10 @@ int launch_tiles_as(const GemmParams &p, bool dots, bool lds, hipStream_t s)
         FG_HIP(hipGetLastError());
         return FG_OK;
     }
+    // the fused scaling over few 32 x 32 tiles: four waves per tile on its quarters (512 x 4864 ->
+    // 896: 25.7 against 33.2 us for one wave per tile; the exact order keeps the split kernel below,
+    // as fast or faster there: 24.0 against 27.3 us)
+    if (FUSED && !dots && lds && p.M > 16 && narrow_waves < 2048) return launch_quarter<FMT, 2, true>(p, s);
     const size_t smem = size_t(p.B) * 32 * 4;
     // too few 32 x 32 tiles for two waves per SIMD: four waves per tile
     const size_t split_smem = smem + 2 * 4 * 4 * 64 * 16;

@@ -126,3 +126,27 @@ def test_row_bands_over_a_long_k(fk, dtype, rows, n, k):
     fk.matmul(m, inp, range(lo, hi), bias=dev(bias), out=h, accumulate=True)
     want_b = oracle(dtype, n, k, data, x, rows, lo, hi, bias=bias)
     assert same_bits(host(h), (h0 + want_b).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
+@pytest.mark.parametrize("rows,n,k", [(17, 36, 256), (40, 260, 4864), (158, 1152, 896), (512, 896, 4864)])
+def test_fused_scaling_over_few_tiles(fk, dtype, rows, n, k):
+    """The NEON backend's scaling over few 32 x 32 tiles (four waves per tile on its 16 x 16 quarters):
+    a last row and column tile that end inside the tile, an odd number of stages, bias and the
+    residual form, against the oracle's fused product."""
+    print(f"fused few tiles dtype {dtype} {rows}x{k}->{n}", flush=True)
+    data = synthetic_table(dtype, n, k, seed=rows + n + k + 2)
+    t = fk.Table(fk.Tensor(dtype, [n, k], data))
+    m = t.matrix()
+    x = activations(rows, k, seed=rows + 2 * k, outliers=0.01)
+    width = (n + 3) // 4 * 4
+    want = oracle(dtype, n, k, data, x, rows, fused=True)
+    got = host(fk.matmul(m, fk.Input(f32=dev(x.reshape(-1))), range(0, width), fused=True))
+    assert same_bits(got, want), first_mismatch(got, want)
+    inp = fk.QuantizedRows().input(m, dev(x.reshape(-1)))
+    bias = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    h0 = np.random.default_rng(k).standard_normal((rows, width - 4)).astype(np.float32)
+    h = dev(h0)
+    fk.matmul(m, inp, range(4, width), bias=dev(bias), out=h, accumulate=True, fused=True)
+    want_b = oracle(dtype, n, k, data, x, rows, 4, width, bias=bias, fused=True)
+    assert same_bits(host(h), (h0 + want_b).astype(np.float32))

@@ -534,11 +534,14 @@ def extras(fk, torch, np, with_cpu=True):
                 np, Q8B32, n, k, data, xh[:cpu_rows], lambda ms_: cpu_ops / ms_ / 1e9, "TOPS",
                 f"the first {cpu_rows} of {rows} rows (rows are independent), f32 rows quantized first")
         res[label] = entry
-    # 3. packed int4 14336 x 4096, rows 1 and 16
+    # 3. packed int4 14336 x 4096, rows 1 and 16: resident (one table, replayed from the 256 MiB
+    #    Infinity Cache) and streamed (distinct copies read in turn, more bytes than that cache holds)
     n, k = 14336, 4096
     data = synthetic_table(np, Q4B32, n, k, rng)
     t = fk.Table(fk.Tensor(Q4B32, [n, k], data))
     m = t.matrix()
+    copies = [fk.Table.from_device_bytes(Q4B32, n, k, torch.from_numpy(data).cuda()) for _ in range(9)]
+    cmats = [c.matrix() for c in copies]
     for rows in (1, 16):
         xh = rng.standard_normal((rows, k)).astype(np.float32)
         x = torch.from_numpy(xh).cuda()
@@ -546,16 +549,24 @@ def extras(fk, torch, np, with_cpu=True):
         out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
         ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 50, graph=True)
         b = n * k // 2 + n * k // 32 * 4 + rows * (k + k // 32 * 8) + rows * n * 4
+        ms_s = timer(lambda: [fk.matmul(cm, inp, range(0, n), out=out) for cm in cmats], 5, graph=True) / len(cmats)
         entry = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
-                 "bytes": b}
+                 "bytes": b, "resident": "one table replayed (it fits the 256 MiB Infinity Cache)",
+                 "streamed_us": round(ms_s * 1e3, 2), "streamed_GB_s": round(b / ms_s / 1e6, 1),
+                 "streamed_frac_hbm": round(b / ms_s / 1e6 / HBM_PEAK_GBS, 4),
+                 "streamed": f"{len(cmats)} distinct copies ({len(cmats) * len(data) / 1e6:.0f} MB) read in turn"}
         if with_cpu:
             entry["cpu_baseline"] = cpu_product_baseline(np, Q4B32, n, k, data, xh, lambda ms_: b / ms_ / 1e6, "GB/s",
                                                          f"the whole product, {rows} f32 row(s) quantized first")
         res[f"int4_14336x4096_rows{rows}"] = entry
-    # 3b. ternary T2b128 14336 x 4096 (2 bits a weight, a scale per 128), rows 1 and 16
+    del copies, cmats
+    # 3b. ternary T2b128 14336 x 4096 (2 bits a weight, a scale per 128), rows 1 and 16, resident and
+    #     streamed
     data = synthetic_table(np, T2B128, n, k, rng)
     t = fk.Table(fk.Tensor(T2B128, [n, k], data))
     m = t.matrix()
+    copies = [fk.Table.from_device_bytes(T2B128, n, k, torch.from_numpy(data).cuda()) for _ in range(20)]
+    cmats = [c.matrix() for c in copies]
     for rows in (1, 16):
         xh = rng.standard_normal((rows, k)).astype(np.float32)
         x = torch.from_numpy(xh).cuda()
@@ -563,12 +574,17 @@ def extras(fk, torch, np, with_cpu=True):
         out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
         ms = timer(lambda: fk.matmul(m, inp, range(0, n), out=out), 50, graph=True)
         b = n * k // 4 + n * k // 128 * 4 + rows * (k + k // 128 * 8) + rows * n * 4
+        ms_s = timer(lambda: [fk.matmul(cm, inp, range(0, n), out=out) for cm in cmats], 5, graph=True) / len(cmats)
         entry = {"us": round(ms * 1e3, 2), "GB_s": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
-                 "bytes": b}
+                 "bytes": b, "resident": "one table replayed (it fits the 256 MiB Infinity Cache)",
+                 "streamed_us": round(ms_s * 1e3, 2), "streamed_GB_s": round(b / ms_s / 1e6, 1),
+                 "streamed_frac_hbm": round(b / ms_s / 1e6 / HBM_PEAK_GBS, 4),
+                 "streamed": f"{len(cmats)} distinct copies ({len(cmats) * len(data) / 1e6:.0f} MB) read in turn"}
         if with_cpu:
             entry["cpu_baseline"] = cpu_product_baseline(np, T2B128, n, k, data, xh, lambda ms_: b / ms_ / 1e6, "GB/s",
                                                          f"the whole product, {rows} f32 row(s) quantized first")
         res[f"t2_14336x4096_rows{rows}"] = entry
+    del copies, cmats
     # 3c. the same T2b128 table times 512 rows (prefill-sized: the matrix cores)
     rows, cpu_rows = 512, 16
     xh = rng.standard_normal((rows, k)).astype(np.float32)

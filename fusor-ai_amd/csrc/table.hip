@@ -331,25 +331,40 @@ namespace {
 // quantize_rows_kernel<8>'s arithmetic for groups of 32, the scale of group g of row r stored at
 // as_t[g·Mpad + r]; the slots of rows M..Mpad-1 get zero scales. Teams of 8 lanes take the
 // (row, group) pairs row first, so a wave's scale stores are one run of a group's column and each
-// team reads its row's group as one 128-byte line.
-__global__ void quantize_rows_t_kernel(const float *__restrict__ x, unsigned M, unsigned G, unsigned Mpad,
+// team reads its row's group as one 128-byte line. Each team takes kQuantPairs pairs, `slice`
+// apart, their loads issued together (more bytes in flight per lane).
+constexpr int kQuantPairs = 4;
+
+__global__ void quantize_rows_t_kernel(const float *__restrict__ x, unsigned M, unsigned G, unsigned Mpad, unsigned slice,
                                        int8_t *__restrict__ q, float *__restrict__ as_t)
 {
     const unsigned t = blockIdx.x * blockDim.x + threadIdx.x;  // 32-bit: the host keeps the lanes below 2^31
-    const unsigned team = t / 8, gi = team / Mpad, r = team - gi * Mpad;
+    const unsigned team0 = t / 8;
+    if (team0 >= slice) return;  // the grid's last threads (a whole team at a time)
     const int sub = int(t % 8);
-    const bool active = r < M && gi < G;
-    const size_t g = size_t(r) * G + gi;
-    const float4 v = active ? reinterpret_cast<const float4 *>(x)[g * 8 + sub] : make_float4(0, 0, 0, 0);
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = max8(fmaxf(0.0f, amax));
-    int l0, l1, l2, l3;
-    const float d = scale_and_levels(amax, v.x, v.y, v.z, v.w, l0, l1, l2, l3);
-    if (active) {
-        reinterpret_cast<int *>(q)[g * 8 + sub] = pack4(l0, l1, l2, l3);
-        if (sub == 0) as_t[size_t(gi) * Mpad + r] = d;
-    } else if (gi < G && sub == 0) {
-        as_t[size_t(gi) * Mpad + r] = 0.0f;
+    float4 v[kQuantPairs];
+    unsigned gi[kQuantPairs], r[kQuantPairs];
+    bool active[kQuantPairs];
+#pragma unroll
+    for (int j = 0; j < kQuantPairs; j++) {
+        const unsigned team = team0 + unsigned(j) * slice;
+        gi[j] = team / Mpad;
+        r[j] = team - gi[j] * Mpad;
+        active[j] = r[j] < M && gi[j] < G;
+        v[j] = active[j] ? reinterpret_cast<const float4 *>(x)[(size_t(r[j]) * G + gi[j]) * 8 + sub] : make_float4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kQuantPairs; j++) {
+        float amax = fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+        amax = max8(fmaxf(0.0f, amax));
+        int l0, l1, l2, l3;
+        const float d = scale_and_levels(amax, v[j].x, v[j].y, v[j].z, v[j].w, l0, l1, l2, l3);
+        if (active[j]) {
+            reinterpret_cast<int *>(q)[(size_t(r[j]) * G + gi[j]) * 8 + sub] = pack4(l0, l1, l2, l3);
+            if (sub == 0) as_t[size_t(gi[j]) * Mpad + r[j]] = d;
+        } else if (gi[j] < G && sub == 0) {
+            as_t[size_t(gi[j]) * Mpad + r[j]] = 0.0f;
+        }
     }
 }
 
@@ -359,10 +374,11 @@ int launch_quantize_rows_t(const float *x, size_t rows, size_t K, int dtype, int
                            hipStream_t s)
 {
     if (group_of(dtype) != 32) return set_error(FG_ERR_FORMAT, "block-major scales take groups of 32");
-    const size_t G = K / 32, threads = Mpad * G * 8;
-    if (threads == 0) return FG_OK;
-    if (threads >= (size_t(1) << 31) || rows > Mpad) return set_error(FG_ERR_SHAPE, "at most 2^31 - 1 quantization lanes in one launch");
-    quantize_rows_t_kernel<<<unsigned((threads + 255) / 256), 256, 0, s>>>(x, unsigned(rows), unsigned(G), unsigned(Mpad), q, as_t);
+    const size_t G = K / 32, teams = Mpad * G, slice = (teams + kQuantPairs - 1) / kQuantPairs, threads = slice * 8;
+    if (teams == 0) return FG_OK;
+    if (teams * 8 >= (size_t(1) << 31) || rows > Mpad) return set_error(FG_ERR_SHAPE, "at most 2^31 - 1 quantization lanes in one launch");
+    quantize_rows_t_kernel<<<unsigned((threads + 255) / 256), 256, 0, s>>>(x, unsigned(rows), unsigned(G), unsigned(Mpad),
+                                                                            unsigned(slice), q, as_t);
     FG_HIP(hipGetLastError());
     return FG_OK;
 }

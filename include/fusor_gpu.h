@@ -189,7 +189,10 @@ typedef struct {
  * and output column c in [col_begin, col_end) (whole quads, within the table's padded rows),
  * out[r * ld_out + (c - col_begin)] = row r · W[c] (+ bias[c] when `bias` is set), written, or
  * added with FG_ACCUMULATE. f32 results are bit-identical to the reference's scalar backend, or
- * with FG_FUSED_SCALE to its NEON backend. */
+ * with FG_FUSED_SCALE to its NEON backend. Products that quantize f32 rows on the matrix cores take
+ * scratch from a stream-ordered pool; under HIP graph capture they take it once, outside the
+ * stream's work, owned by the graph (no memory node; two instances of one graph must not run at
+ * once), and it is freed after the graph is destroyed. */
 int fg_matmul(const fg_table *table, const fg_input *input, size_t rows, size_t col_begin,
               size_t col_end, const float *bias, float *out, size_t ld_out, int flags, void *stream);
 

@@ -449,4 +449,7 @@ int launch_gemm_batch(const ProductArgs &a, int items, int per_table, int first,
                       size_t out_stride, size_t codes_stride, size_t scales_stride, hipStream_t s);
 int launch_t2(const ProductArgs &a, hipStream_t s);
 int launch_product(const ProductArgs &a, hipStream_t s);
+// Two products of the same pre-quantized rows over tables of one shape (a layer's gate and up):
+// one launch when both take the same kernel, else one each.
+int launch_product_pair(const ProductArgs &a, const ProductArgs &b, hipStream_t s);
 }  // namespace fg

@@ -50,6 +50,12 @@ struct GemmParams {
     // a batch of products (the staged kernel's grid y): item z takes the levels, scales and outputs
     // z items on (strides in elements) and table z / per_table's codes and scales
     long q_batch, as_batch, out_batch, codes_batch, wscales_batch;
+    // a second product of the same rows in the same launch (the split kernel): workgroups from
+    // tiles1 on take this table and output instead (gate and up of one input)
+    const int8_t *codes2;
+    const float *wscales2;
+    float *out2;
+    int tiles1;
     int per_table, first;  // item z's table: (z + first) / per_table − first / per_table on
 };
 
@@ -265,8 +271,15 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmParams p)
     v4f *terms = reinterpret_cast<v4f *>(split_lds + B * 32);
     const int tid = threadIdx.x, lane = tid & 63, i = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int L = int(blockIdx.x);
+    if (p.codes2 && L >= p.tiles1) {  // the launch's second product (uniform per workgroup)
+        L -= p.tiles1;
+        p.codes = p.codes2;
+        p.wscales = p.wscales2;
+        p.out = p.out2;
+    }
     int tx, ty;
-    tile_of(int(blockIdx.x), (p.col_end - p.col_begin + 31) / 32, (p.M + 31) / 32, tx, ty);
+    tile_of(L, (p.col_end - p.col_begin + 31) / 32, (p.M + 31) / 32, tx, ty);
     const int m0 = ty * 32, n0 = p.col_begin + tx * 32;
     const int row = min(m0 + i, p.M - 1);
     const int8_t *arow = p.q + size_t(row) * p.K + h * 16;
@@ -2236,6 +2249,53 @@ static bool on_matvec(const ProductArgs &a)
 {
     // the matrix-vector kernel sums separately rounded terms; the fused scaling runs on the tiles
     return a.t->dtype != FG_T2B128 && a.rows <= 4 && !a.fused;
+}
+
+// Two products of the same pre-quantized rows over tables of one shape and format (a layer's gate
+// and up): one launch of the split kernel over both when that is the kernel each would take, else
+// one launch each.
+int launch_product_pair(const ProductArgs &a, const ProductArgs &b, hipStream_t s)
+{
+    const fg_table *t = a.t, *u = b.t;
+    const long ncols = long(a.quad_end - a.quad_begin) * 4;
+    const long narrow = ((ncols + 31) / 32) * ((long(a.rows) + 31) / 32);
+    const size_t split_smem = size_t(t->groups) * 32 * 4 + 2 * 4 * 4 * 64 * 16;
+    const bool split = t->dtype == u->dtype && t->cols == u->cols && t->rows == u->rows && a.rows == b.rows && a.q == b.q &&
+                       a.as == b.as && a.q && !a.x && !b.x && !a.dots && !b.dots && !a.fused && !b.fused && !a.bias && !b.bias &&
+                       !a.workspace && !b.workspace && a.quad_begin == b.quad_begin && a.quad_end == b.quad_end &&
+                       a.accumulate == b.accumulate && a.ld_out == b.ld_out &&
+                       (t->dtype == FG_Q7B32 || t->dtype == FG_Q8B32 || t->dtype == FG_Q4B32) && a.rows > 16 &&
+                       !on_matvec(a) && choose_tiles(a) == 0 && t->groups % 4 == 0 && t->groups * 32 * 4 <= 64 * 1024 &&
+                       (reinterpret_cast<uintptr_t>(a.as) & 15) == 0 && narrow < 2048 && split_smem <= 64 * 1024 &&
+                       !(a.rows <= 256 && t->blocks >= 64) && 2 * narrow < (long(1) << 31);
+    if (!split) {
+        const int rc = launch_product(a, s);
+        return rc ? rc : launch_product(b, s);
+    }
+    GemmParams p{};
+    p.codes = t->codes;
+    p.wscales = t->scales;
+    p.B = int(t->blocks);
+    p.G = int(t->groups);
+    p.K = int(t->cols);
+    p.M = int(a.rows);
+    p.Mpad = int((a.rows + 63) / 64 * 64);
+    p.col_begin = int(a.quad_begin * 4);
+    p.col_end = int(a.quad_end * 4);
+    p.n_rows = int(t->rows);
+    p.q = a.q;
+    p.as = a.as;
+    p.out = a.out;
+    p.ld_out = long(a.ld_out);
+    p.accumulate = a.accumulate;
+    p.codes2 = u->codes;
+    p.wscales2 = u->scales;
+    p.out2 = b.out;
+    p.tiles1 = int(narrow);
+    if (t->dtype == FG_Q4B32) gemm_split_kernel<4><<<dim3{unsigned(2 * narrow)}, 256, split_smem, s>>>(p);
+    else gemm_split_kernel<8><<<dim3{unsigned(2 * narrow)}, 256, split_smem, s>>>(p);
+    FG_HIP(hipGetLastError());
+    return FG_OK;
 }
 
 int launch_product(const ProductArgs &a, hipStream_t s)

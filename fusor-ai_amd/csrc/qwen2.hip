@@ -154,16 +154,16 @@ __device__ float attn_block_sum(float v, float *red)
     return ((red[4] + red[5]) + red[6]) + red[7];
 }
 
-// kWeighKeys keys x kWeighDims dims of one KV head's values into registers (8 float4 per thread),
-// branch-free.
+// kWeighKeys keys x kWeighDims dims of one KV head's values into registers (8 float4 per thread);
+// rows past the n keys are not read (a prefill's early rows see few keys).
 __device__ __forceinline__ void fetch_values(const float *vbase, int capacity, int D, int d0, int j0, int n, float4 *r)
 {
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const int e = int(threadIdx.x) + k * kAttnThreads;  // float4 index: row e / 8, column (e % 8) * 4
         const int row = e >> 3, c4 = e & 7;
-        const int rr = row < n ? row : 0;
-        r[k] = *reinterpret_cast<const float4 *>(vbase + size_t((j0 + rr) % capacity) * D + d0 + c4 * 4);
+        r[k] = row < n ? *reinterpret_cast<const float4 *>(vbase + size_t((j0 + row) % capacity) * D + d0 + c4 * 4)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 }
 
@@ -980,8 +980,24 @@ int prefill_layer(fg_qwen2 *m, size_t li, size_t first, int n, hipStream_t st)
     if ((rc = prefill_product(m, ly.o, n, nullptr, m->pre.x, sh.hidden, true, st))) return rc;
     // hidden += down(silu(gate(x))·up(x)), x the normed rows (layer.rs:249-344)
     if ((rc = prefill_norm(m, ly.norm2, n, st))) return rc;
-    if ((rc = prefill_product(m, ly.gate, n, nullptr, m->pre.gate, sh.ffn, false, st))) return rc;
-    if ((rc = prefill_product(m, ly.up, n, nullptr, m->pre.up, sh.ffn, false, st))) return rc;
+    {
+        // gate and up of the same rows, one launch where the kernel allows it
+        ProductArgs g{}, u{};
+        g.t = ly.gate;
+        u.t = ly.up;
+        for (ProductArgs *a : {&g, &u}) {
+            a->q = m->pre.lev;
+            a->as = m->pre.lsc;
+            a->corr = m->pre.lco;
+            a->rows = size_t(n);
+            a->quad_begin = 0;
+            a->quad_end = a->t->quads;
+            a->ld_out = sh.ffn;
+        }
+        g.out = m->pre.gate;
+        u.out = m->pre.up;
+        if ((rc = launch_product_pair(g, u, st))) return rc;
+    }
     const size_t groups = size_t(n) * sh.ffn / 32;
     swiglu_quantize_kernel<<<unsigned((groups * 8 + 255) / 256), 256, 0, st>>>(m->pre.gate, m->pre.up, groups, m->zp, m->pre.lev,
                                                                               m->pre.lsc, m->pre.lco);

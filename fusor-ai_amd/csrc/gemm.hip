@@ -2052,7 +2052,12 @@ int launch_t2(const ProductArgs &a, hipStream_t s)
     // the matrix cores for many rows, the streamed kernel for few (the int32 dots stay on the
     // one-thread-per-output kernel)
     const bool fused = a.fused != 0;
-    const bool tiles16 = M >= kT2Gemm16Rows && M <= kT2Gemm16MaxRows;
+    // 5-16 rows take the 16 x 16 tiles over many columns; over few the tiles are too few waves and
+    // the streamed kernel's row slices are faster (896 x 4864 at 5-16 rows: 6.1 against 9.4 us;
+    // 4096 x 1024: 3.7 against 4.0 at 5-8 rows, 4.4 against 4.3 at 12; 14336 x 4096 at 5 rows:
+    // 9.6 against 15.3)
+    const int ctiles = (ncols + 15) / 16;
+    const bool tiles16 = M >= kT2Gemm16Rows && M <= kT2Gemm16MaxRows && (ctiles >= 300 || (M >= 9 && ctiles >= 256));
     if (rc == FG_OK && !a.dots && (tiles16 || M >= kT2GemmRows) && size_t(G) * 32 * 8 <= 64 * 1024 &&
         (reinterpret_cast<uintptr_t>(q) & 15) == 0) {
         T2Params p{};

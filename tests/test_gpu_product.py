@@ -396,8 +396,8 @@ def test_int4_shape_bit_exact(fk, rows):
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("n_rows,cols", [(70, 384), (37, 1152), (18, 5120), (9, 128), (5, 16384)])
 def test_t2_streamed_chunks_rings_and_row_slices(fk, rows, n_rows, cols):
-    """T2b128 products of up to 8 rows: 1-4 rows on the streamed kernel (slices of 1, 2 or 4 rows),
-    5 and 8 rows on the 16 x 16 matrix-core tiles; 3 groups (one partial 1 KiB chunk), 9 groups (a
+    """T2b128 products of up to 8 rows over few columns, on the streamed kernel (slices of 1, 2 or 4
+    rows); 3 groups (one partial 1 KiB chunk), 9 groups (a
     second chunk of one group), 40 groups (five chunks: the four-chunk ring refilled), one group,
     and 128 groups (16384 levels a row: slices of two rows, not four, to fit the workgroup's LDS);
     70 outputs (a last workgroup of two quads); bias and the fused scaling."""
@@ -446,6 +446,29 @@ def test_t2_on_the_matrix_cores(fk, rows, n_rows, cols):
     want_r = oracle_product(dtype, n_rows, cols, data, x, rows, lo, hi)
     got_r = gpu_product(fk, t, x, rows, cols=range(lo, hi))
     assert same_bits(got_r, want_r), first_mismatch(got_r, want_r)
+
+
+@pytest.mark.parametrize("rows", [5, 8, 12, 16])
+@pytest.mark.parametrize("n", [4864, 4096])
+def test_t2_small_batches_by_width(fk, rows, n):
+    """5-16 rows: over 4864 columns (304 tiles of 16) the 16 x 16 matrix-core tiles, over 4096 (256
+    tiles) the streamed row slices up to 8 rows and the tiles from 9; every output, bias, a column
+    range, the fused scaling."""
+    print(f"t2 small batch {rows} x 512 -> {n}", flush=True)
+    dtype, k = O.T2B128, 512
+    data = synthetic_table(dtype, n, k, seed=n + rows)
+    t = table(fk, dtype, n, k, data)
+    x = activations(rows, k, seed=rows + 7, outliers=0.02)
+    bias = np.random.default_rng(rows).standard_normal(n).astype(np.float32)
+    want = oracle_product(dtype, n, k, data, x, rows, bias=bias)
+    got = gpu_product(fk, t, x, rows, bias=bias)
+    assert same_bits(got, want), first_mismatch(got, want)
+    want_r = oracle_product(dtype, n, k, data, x, rows, 64, n - 4)
+    got_r = gpu_product(fk, t, x, rows, cols=range(64, n - 4))
+    assert same_bits(got_r, want_r), first_mismatch(got_r, want_r)
+    want_f = oracle_product(dtype, n, k, data, x, rows, fused=True)
+    got_f = gpu_product(fk, t, x, rows, fused_scale=True)
+    assert same_bits(got_f, want_f), first_mismatch(got_f, want_f)
 
 
 def test_t2_many_tiles_bit_exact(fk):

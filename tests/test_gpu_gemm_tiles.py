@@ -1,11 +1,14 @@
-"""The LDS-staged matrix-core product (gemm_lds_kernel) at each of its tile shapes, against the oracle.
+"""The batched matrix-core products at each of their kernel choices, against the oracle.
 
-The product picks its kernel by shape; FG_GEMM_TILE forces one (0: the register-ring kernels, 11:
-64 x 64 workgroup tiles, 21: 128 x 64), so every tile shape meets the edge cases here: rows and
-columns that end inside a tile, an odd number of blocks (the last two-block stage half empty), a
-column range that starts inside the table, bias and the residual form, f32 and pre-quantized rows,
-the NEON backend's fused scaling, and scale products fl(ws * as) that are subnormal (the tile
-forms them with an f32 MFMA outer product, which must round them as the VALU does).
+The product picks its kernel by shape; FG_GEMM_TILE forces one (0: the register-ring kernels, which
+over few 32 x 32 tiles and a multiple of four blocks are the four-wave split kernel; 11: the
+LDS-staged kernel's 64 x 64 workgroup tiles, 21: its 128 x 64), so every choice meets the edge
+cases here: rows and columns that end inside a tile, an odd number of blocks (the last two-block
+stage half empty) or of rounds of four blocks (the split kernel's last pair of rounds half
+empty), activation scales staged in LDS (more than 64 blocks) or read with the operands, a column
+range that starts inside the table, bias and the residual form, f32 and pre-quantized rows, the
+NEON backend's fused scaling, and scale products fl(ws * as) that are subnormal (both kernels form
+them with an f32 MFMA outer product, which must round them as the VALU does).
 """
 
 import numpy as np
@@ -16,7 +19,7 @@ from gpu_data import activations, synthetic_table
 
 pytestmark = pytest.mark.gpu
 
-TILES = ["11", "21"]
+TILES = ["0", "11", "21"]
 
 
 @pytest.fixture(scope="module")
@@ -56,7 +59,7 @@ def oracle(dtype, n, k, data, x, rows, col_begin=0, col_end=None, bias=None, fus
 
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
-@pytest.mark.parametrize("rows,n,k", [(17, 36, 32), (100, 200, 160), (257, 516, 1152), (130, 2050, 96)])
+@pytest.mark.parametrize("rows,n,k", [(17, 36, 32), (100, 200, 160), (257, 516, 1152), (130, 2050, 96), (300, 260, 2176)])
 def test_tile_shapes_bit_exact(fk, monkeypatch, tile, dtype, rows, n, k):
     monkeypatch.setenv("FG_GEMM_TILE", tile)
     print(f"tile {tile} dtype {dtype} {rows}x{k}->{n}", flush=True)

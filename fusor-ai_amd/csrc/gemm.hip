@@ -324,9 +324,10 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmParams p)
     // their latencies overlap; so is the outer product of the next pair, at its first round.
     v16i d;
     v32f pp;  // the pair's scale products: round r's at [16 (r & 1) + v], laid out as d
-    auto issue = [&](int r, const Op &o, auto first_of_pair) {
+    // this lane's activation scale for the outer product of the pair that starts at round r
+    auto pair_as = [&](int r, const Op &o) { return STAGE ? tile_scales[min(4 * (r + h) + wave, B - 1) * 32 + i] : o.as; };
+    auto issue = [&](const Op &o, auto first_of_pair, float asv) {
         if constexpr (decltype(first_of_pair)::value) {
-            const float asv = STAGE ? tile_scales[min(4 * (r + h) + wave, B - 1) * 32 + i] : o.as;
             const v32f zero32 = {0};
             pp = __builtin_amdgcn_mfma_f32_32x32x1f32(asv, o.ws, zero32, 0, 0, 0);
         }
@@ -340,9 +341,12 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmParams p)
         asm volatile("" : "+v"(d));  // keeps the product here rather than sunk to its first use
     };
     // round r (parity P): its terms to LDS, `o` refilled with round r + 2, the barrier, then the
-    // round's four groups added in order to this wave's quarter of the outputs
+    // round's four groups added in order to this wave's quarter of the outputs. The next pair's
+    // activation scale is read before the barrier, so that after it the term reads go out first
+    // and the products follow without waiting on LDS.
     auto round = [&](int r, Op &o, const Op &o_next, auto parity) {
         constexpr int P = decltype(parity)::value;
+        const float asn = P == 1 ? pair_as(r + 1, o_next) : 0.0f;
         v4f *buf = terms + P * (4 * 4 * 64);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -354,7 +358,8 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmParams p)
         __syncthreads();
         const v4f t0 = buf[wave * 64 + lane], t1 = buf[(4 + wave) * 64 + lane], t2 = buf[(8 + wave) * 64 + lane],
                   t3 = buf[(12 + wave) * 64 + lane];
-        issue(r + 1, o_next, std::integral_constant<bool, P == 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        issue(o_next, std::integral_constant<bool, P == 1>{}, asn);
         __builtin_amdgcn_sched_barrier(0);  // the products go out before the additions wait
         acc[0] = acc[0] + t0.x + t1.x + t2.x + t3.x;
         acc[1] = acc[1] + t0.y + t1.y + t2.y + t3.y;
@@ -364,7 +369,7 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmParams p)
     // whole pairs of rounds without a branch (the load counts the compiler waits on stay exact),
     // then an odd last round
     const int rounds = B / 4;
-    issue(0, ring[0], std::true_type{});
+    issue(ring[0], std::true_type{}, pair_as(0, ring[0]));
     int r0 = 0;
     for (; r0 + 2 <= rounds; r0 += 2) {
         round(r0, ring[0], ring[1], std::integral_constant<int, 0>{});

@@ -1914,13 +1914,6 @@ struct ScratchPlan {
     size_t total() const { return q_bytes + 2 * s_bytes + t_bytes; }
 };
 
-// Workgroups of the LDS-staged kernel at a tile shape.
-static long lds_groups(const ProductArgs &a, int wm, int wn)
-{
-    const long cols = long(a.quad_end - a.quad_begin) * 4, rows = long(a.rows);
-    return ((cols + 64 * wn - 1) / (64 * wn)) * ((rows + 64 * wm - 1) / (64 * wm));
-}
-
 // The kernel of a batched product: 0 for the register-ring kernels, else the LDS-staged kernel's
 // tile shape. FG_GEMM_TILE (0, 11 or 21) overrides the choice, for tests and measurements.
 static int choose_tiles(const ProductArgs &a)
@@ -1937,9 +1930,10 @@ static int choose_tiles(const ProductArgs &a)
     // few 32 x 32 tiles: four waves per tile over alternate groups (gemm_split_kernel), or for the
     // fused scaling one wave per tile (gemm_kernel)
     if (narrow < 2048 && (a.fused || (t->groups % 4 == 0 && split_smem <= 64 * 1024))) return 0;
-    // 128 x 64 workgroup tiles while they still make two rounds of workgroups (four per CU),
-    // else 64 x 64 (measured on the DiT block's 4096-row products and 512-row prefill)
-    return lds_groups(a, 2, 1) >= 1536 ? 21 : 11;
+    // 64 x 64 workgroup tiles. The 128 x 64 tiles (kept for FG_GEMM_TILE=21) measured 3-6 %
+    // slower on the DiT block's 4096-row products, 15-17 % at 512 x 896 -> 9728 and 8192 x 4608 ->
+    // 1152, and even at 16384 x 1152 -> 4608.
+    return 11;
 }
 
 ScratchPlan plan_scratch(const ProductArgs &a)

@@ -323,6 +323,185 @@ __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
     return s;
 }
 
+// A prefill's attention, per (head, block of R = 256 / D rows): each row's scores against the keys
+// up to its own position (ops.rs:310-326: dot_f32 in index order from -0, times 1/sqrt(D); one
+// thread per row and key), its softmax (ops.rs:301-306: maximum, ops::exp, the total, the division;
+// a wave per row, the total in key order by one lane when exact, else a wave tree), its weighted
+// values in key order from +0 (ops.rs:329-342, one thread per row and value dimension), then its
+// outputs quantized per group of 32 for the output projection. The block's rows share one KV
+// head's keys and values, staged once per pass of 4096 / D keys for all of them.
+// LDS: the rows' scores, then weights [R][kstride]; a pass of keys [4096 / D][D + 1] or values
+// [4096 / D][D] (then the outputs [R][D]); the query rows [R][D]; the totals [R].
+template <bool EXACT>
+__global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(AttnParams a, int n, int kstride)
+{
+    extern __shared__ __align__(16) float ash[];
+    const int D = a.D, R = kAttnThreads / D, KC = 4096 / D, S = D + 1;
+    const int head = blockIdx.x, z0 = int(blockIdx.y) * R;
+    const int kv = head / (a.heads / a.kv_heads);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *w = ash;
+    float *stage = w + R * kstride;
+    float *qrows = stage + KC * S;
+    float *tot = qrows + R * D;
+    const float *kbase = a.kcache + a.layer_base + size_t(kv) * a.capacity * D;
+    const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D;
+    const int rows = min(R, n - z0);
+    const int kblock = a.keys + z0 + rows - 1;  // keys of the block's last row, the most
+    // Passes 0 .. P - 1 stage keys, P .. 2P - 1 values, KC rows each: every thread's share (at most
+    // four float4s) of pass p + 1 is loaded into registers while pass p is worked on.
+    const int P = (kblock + KC - 1) / KC, D4 = D / 4;
+    float4 ahead[4];
+    auto load_pass = [&](int p) {
+        const float *base = p < P ? kbase : vbase;
+        const int c0 = (p < P ? p : p - P) * KC, nk = min(KC, kblock - c0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = tid + k * kAttnThreads, row = e / D4;
+            if (row < nk) ahead[k] = *reinterpret_cast<const float4 *>(base + size_t((c0 + row) % a.capacity) * D + (e - row * D4) * 4);
+        }
+    };
+    auto store_pass = [&](int p) {
+        const int nk = min(KC, kblock - (p < P ? p : p - P) * KC);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = tid + k * kAttnThreads, row = e / D4;
+            if (row >= nk) continue;
+            if (p < P) {  // keys: rows D + 1 floats apart
+                float *dst = stage + row * S + (e - row * D4) * 4;
+                dst[0] = ahead[k].x;
+                dst[1] = ahead[k].y;
+                dst[2] = ahead[k].z;
+                dst[3] = ahead[k].w;
+            } else {
+                reinterpret_cast<float4 *>(stage)[e] = ahead[k];
+            }
+        }
+    };
+    load_pass(0);
+    for (int e = tid; e < rows * D; e += kAttnThreads) {
+        const int r = e / D;
+        qrows[e] = a.qkv[size_t(z0 + r) * a.qkv_stride + size_t(head) * D + (e - r * D)];
+    }
+    // scores (pairs key-fastest: neighbouring lanes read neighbouring key rows, D + 1 floats
+    // apart, and one query row)
+    const float scale = 1.0f / sqrtf(float(D));
+    for (int p = 0; p < P; p++) {
+        const int c0 = p * KC, nk = min(KC, kblock - c0);
+        __syncthreads();  // the previous pass's keys are read (the first: the queries are written)
+        store_pass(p);
+        __syncthreads();
+        load_pass(p + 1);
+        for (int pr = tid; pr < rows * nk; pr += kAttnThreads) {
+            const int r = pr / nk, j = pr - r * nk;
+            if (c0 + j >= a.keys + z0 + r) continue;  // past the row's own position
+            const float *q = qrows + r * D, *k = stage + j * S;
+            float sum = -0.0f;
+            for (int d = 0; d < D; d += 16) {
+                float x[16], y[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    x[e] = q[d + e];
+                    y[e] = k[d + e];
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) sum = sum + x[e] * y[e];
+            }
+            w[r * kstride + c0 + j] = sum * scale;
+        }
+    }
+    __syncthreads();
+    for (int r = wave; r < rows; r += kAttnThreads / 64) {
+        const int keys = a.keys + z0 + r;
+        float *wr = w + r * kstride;
+        float m = -INFINITY;
+        for (int j = lane; j < keys; j += 64) m = fmaxf(m, wr[j]);
+        const float peak = wave_allmax(m);
+        float part = 0.0f;
+        for (int j = lane; j < keys; j += 64) {
+            const float e = ref_exp(wr[j] - peak);
+            wr[j] = e;
+            part = part + e;
+        }
+        if (!EXACT) {
+            const float t = wave_allsum(part);
+            if (lane == 0) tot[r] = t;
+        }
+    }
+    __syncthreads();
+    if (EXACT && tid < rows) tot[tid] = chain_sum(-0.0f, a.keys + z0 + tid, w + tid * kstride);
+    __syncthreads();
+    for (int e = tid; e < rows * kstride; e += kAttnThreads) {
+        const int r = e / kstride, j = e - r * kstride;
+        if (j < a.keys + z0 + r) w[e] = w[e] / tot[r];
+    }
+    const int r = tid / D, i = tid - r * D;  // this thread's row and value dimension
+    const bool live = r < rows;
+    const int keys = a.keys + z0 + r;
+    float o = 0.0f;
+    for (int p = P; p < 2 * P; p++) {
+        const int c0 = (p - P) * KC, nk = min(KC, kblock - c0);
+        __syncthreads();  // the weights are final; the previous pass's values are read
+        store_pass(p);
+        __syncthreads();
+        if (p + 1 < 2 * P) load_pass(p + 1);
+        if (live) {
+            // sixteen weights and values read ahead of their sixteen ordered additions
+            const int end = min(nk, keys - c0);
+            const float *wr = w + r * kstride + c0;
+            int j = 0;
+            for (; j + 16 <= end; j += 16) {
+                float ww[16], vv[16];
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    ww[e] = wr[j + e];
+                    vv[e] = stage[(j + e) * D + i];
+                }
+#pragma unroll
+                for (int e = 0; e < 16; e++) o = o + ww[e] * vv[e];
+            }
+            for (; j < end; j++) o = o + wr[j] * stage[j * D + i];
+        }
+    }
+    __syncthreads();
+    if (live) stage[r * D + i] = o;
+    __syncthreads();
+    // the block's rows x D / 32 groups (at most 8), eight lanes each
+    if (tid < 8 * (rows * D / 32)) {
+        const int g = tid >> 3, sub = tid & 7;
+        const int r2 = g * 32 / D, c = g * 32 - r2 * D;
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = stage[r2 * D + c + sub * 4 + e];
+        const size_t at = size_t(z0 + r2) * a.row_width + size_t(head) * D + c;
+        if (a.row_out) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) a.row_out[at + sub * 4 + e] = x[e];
+        }
+        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        amax = max8(fmaxf(0.0f, amax));
+        int l0, l1, l2, l3;
+        const float d = scale_and_levels(amax, x[0], x[1], x[2], x[3], l0, l1, l2, l3);
+        const int sum = sum8(l0 + l1 + l2 + l3);
+        const size_t G = at / 32;
+        reinterpret_cast<int *>(a.q)[G * 8 + sub] = pack4(l0, l1, l2, l3);
+        if (sub == 0) {
+            a.scales[G] = d;
+            a.corr[G] = -a.zp * sum;
+        }
+    }
+}
+
+// LDS of attn_rows_kernel for a prefill whose last row sees kmax keys (0 when it does not fit 64 KiB
+// or the head is wider than a workgroup).
+inline size_t attn_rows_smem(int D, int kmax)
+{
+    const int R = kAttnThreads / D;
+    if (R < 1) return 0;
+    const size_t bytes = (size_t(R) * ((kmax + 3) / 4 * 4) + size_t(4096 / D) * (D + 1) + size_t(R) * D + 16) * 4;
+    return bytes <= 64 * 1024 ? bytes : 0;
+}
+
 // The exact-order attention of one query head for kWeighDims value dimensions (the reference's
 // arithmetic of attn_weigh_kernel<true>, ops.rs:301-342), over the scores of the cached keys that
 // the query launch formed (score_chunk). Grid: (heads, D / kWeighDims), 256 threads.
@@ -969,12 +1148,21 @@ int prefill_layer(fg_qwen2 *m, size_t li, size_t first, int n, hipStream_t st)
     a.scales = m->pre.lsc;
     a.corr = m->pre.lco;
     a.row_width = width;
-    const dim3 sgrid(unsigned(sh.kv_heads), unsigned((first + n + kScoreKeys - 1) / kScoreKeys), unsigned(n));
-    attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
-    FG_HIP(hipGetLastError());
-    const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims), unsigned(n));
-    if (sh.exact) attn_weigh_kernel<true><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
-    else attn_weigh_kernel<false><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
+    const int D = int(sh.head_dim), kmax = int(first) + n;
+    if (const size_t rsmem = attn_rows_smem(D, kmax)) {
+        // blocks of rows sharing their keys and values (each row over its own keys)
+        const int R = kAttnThreads / D;
+        const dim3 rgrid(unsigned(sh.heads), unsigned((n + R - 1) / R));
+        if (sh.exact) attn_rows_kernel<true><<<rgrid, kAttnThreads, rsmem, st>>>(a, n, (kmax + 3) / 4 * 4);
+        else attn_rows_kernel<false><<<rgrid, kAttnThreads, rsmem, st>>>(a, n, (kmax + 3) / 4 * 4);
+    } else {
+        const dim3 sgrid(unsigned(sh.kv_heads), unsigned((first + n + kScoreKeys - 1) / kScoreKeys), unsigned(n));
+        attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
+        FG_HIP(hipGetLastError());
+        const dim3 wgrid(unsigned(sh.heads), unsigned(sh.head_dim / kWeighDims), unsigned(n));
+        if (sh.exact) attn_weigh_kernel<true><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
+        else attn_weigh_kernel<false><<<wgrid, kAttnThreads, m->weigh_smem, st>>>(a);
+    }
     FG_HIP(hipGetLastError());
     // hidden += o(attention) (layer.rs:239-245)
     if ((rc = prefill_product(m, ly.o, n, nullptr, m->pre.x, sh.hidden, true, st))) return rc;

@@ -1930,10 +1930,12 @@ static int choose_tiles(const ProductArgs &a)
     // few 32 x 32 tiles: four waves per tile over alternate groups (gemm_split_kernel), or for the
     // fused scaling one wave per tile (gemm_kernel)
     if (narrow < 2048 && (a.fused || (t->groups % 4 == 0 && split_smem <= 64 * 1024))) return 0;
-    // 64 x 64 workgroup tiles. The 128 x 64 tiles (kept for FG_GEMM_TILE=21) measured 3-6 %
-    // slower on the DiT block's 4096-row products, 15-17 % at 512 x 896 -> 9728 and 8192 x 4608 ->
-    // 1152, and even at 16384 x 1152 -> 4608.
-    return 11;
+    // 64 x 64 workgroup tiles: 128 x 64 measured 3-6 % slower on the DiT block's 4096-row
+    // products, 15-17 % at 512 x 896 -> 9728 and 8192 x 4608 -> 1152, tied at 16384 x 1152 ->
+    // 4608. Over at most four blocks (the int8 attention's scores, 4096 x 96 -> 4096 per head) the
+    // 128 x 64 tiles are kept while they still make 1536 workgroups: 0.96 against 1.00 ms per call.
+    const long tiles21 = ((ncols + 63) / 64) * ((long(a.rows) + 127) / 128);
+    return t->blocks <= 4 && tiles21 >= 1536 ? 21 : 11;
 }
 
 ScratchPlan plan_scratch(const ProductArgs &a)

@@ -102,7 +102,7 @@ def test_exact_read_is_bit_identical_for_every_chunk(fk, dtype, chunk):
 @pytest.mark.parametrize("head_dim,heads,kv_heads", [(64, 4, 1), (128, 2, 2), (32, 6, 3), (128, 12, 2)])
 def test_read_head_sizes(fk, head_dim, heads, kv_heads):
     """Every head size, and rows of heads wider than 1024; 70 rows from position 0 in chunks of 32
-    (scores over blocks of 32 keys: rows that see one, two and three blocks)."""
+    (keys and values staged in passes of 4096 / D rows: rows that see one to three passes)."""
     print(f"prefill heads {heads}/{kv_heads} D {head_dim}", flush=True)
     shape = dict(hidden=256, layers=2, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=512, vocab=64,
                  capacity=128)
@@ -126,6 +126,23 @@ def test_qwen2_half_billion_shape_prefill_of_158_rows(fk, dtype):
     got, want = read_both(fk, dtype, params, ids, 100, 64, exact=True, threads=16)
     assert same_bits(got[0], want[0]) and same_bits(got[1], want[1]) and got[2] == want[2]
     assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+
+
+@pytest.mark.parametrize("first", [1400, 1500])
+def test_read_over_long_caches(fk, first):
+    """Rows that see over a thousand keys: from position 1400 the per-block attention stages its keys
+    and values in a dozen passes; from 1500 the rows' scores no longer fit its LDS and the chunk
+    takes the scores and weighted-sum kernels over its rows instead. Bit-identical in exact order,
+    within the stack tolerance in parallel order."""
+    print(f"prefill from position {first}", flush=True)
+    shape = dict(hidden=128, layers=1, heads=4, kv_heads=2, head_dim=32, ffn=256, vocab=64, capacity=1600)
+    params = qwen2_model(O.Q7B32, seed=first, synthetic=False, **shape)
+    ids = np.random.default_rng(first).integers(0, 64, 40).astype(np.int32)
+    got, want = read_both(fk, O.Q7B32, params, ids, first, 40, exact=True)
+    assert same_bits(got[0], want[0]) and same_bits(got[1], want[1]) and got[2] == want[2]
+    assert same_bits(got[3], want[3]) and same_bits(got[4], want[4])
+    got, want = read_both(fk, O.Q7B32, params, ids, first, 40, exact=False)
+    assert rel_l2(got[0], want[0]) < FAST_TOLERANCE and rel_l2(got[1], want[1]) < FAST_TOLERANCE
 
 
 def test_read_then_decode_continues_the_sequence(fk):

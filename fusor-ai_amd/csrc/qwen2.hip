@@ -40,7 +40,7 @@ constexpr int kWeighDims = 32;   // value dimensions per workgroup (one quantiza
 constexpr int kHeadQuads = 16;  // quads per workgroup of the logits product
 
 struct AttnParams {
-    const float *qkv;  // rotated query heads first
+    const float *qkv;  // query heads first (rotated, except for attn_rows_kernel, which rotates them)
     const float *kcache, *vcache;
     size_t layer_base;
     int heads, kv_heads, D, capacity, keys;
@@ -54,6 +54,10 @@ struct AttnParams {
     // after z such blocks, its outputs (levels, scales, corrections, row_out) z·row_width values on, and
     // keys + z keys (its own position's included)
     size_t qkv_stride, row_width;
+    // a prefill's attention that also rotates its chunk's rows and keeps their keys and values
+    // (attn_rows_kernel): the angles [capacity][D], and the caches written
+    const float *rope;
+    float *kkeep, *vkeep;
 };
 
 // Row blockIdx.z of a prefill's attention: its own query, scores, outputs and key count.
@@ -323,13 +327,18 @@ __device__ __forceinline__ float chain_sum(float s, int n, const float *t)
     return s;
 }
 
-// A prefill's attention, per (head, block of R = 256 / D rows): each row's scores against the keys
-// up to its own position (ops.rs:310-326: dot_f32 in index order from -0, times 1/sqrt(D); one
-// thread per row and key), its softmax (ops.rs:301-306: maximum, ops::exp, the total, the division;
-// a wave per row, the total in key order by one lane when exact, else a wave tree), its weighted
-// values in key order from +0 (ops.rs:329-342, one thread per row and value dimension), then its
-// outputs quantized per group of 32 for the output projection. The block's rows share one KV
-// head's keys and values, staged once per pass of 4096 / D keys for all of them.
+// A prefill's attention, per (head, block of R = 256 / D rows), straight from the chunk's QKV rows
+// (bias added, not yet rotated): each row's query heads rotated by halves at its own position
+// (ops.rs:77-85), its scores against the keys up to that position (ops.rs:310-326: dot_f32 in
+// index order from -0, times 1/sqrt(D); one thread per row and key), its softmax (ops.rs:301-306:
+// maximum, ops::exp, the total, the division; a wave per row, the total in key order by one lane
+// when exact, else a wave tree), its weighted values in key order from +0 (ops.rs:329-342, one
+// thread per row and value dimension), then its outputs quantized per group of 32 for the output
+// projection. The block's rows share one KV head's keys and values, staged once per pass of
+// 4096 / D keys for all of them: the cached rows before the chunk as kept, the chunk's own rows
+// from its QKV rows, keys rotated as they are staged. The workgroup of each KV head's first query
+// head keeps its rows' rotated keys and values in the caches (KvCache::keep, transformer.rs:166-180);
+// no workgroup of the launch reads the caches at the chunk's positions.
 // LDS: the rows' scores, then weights [R][kstride]; a pass of keys [4096 / D][D + 1] or values
 // [4096 / D][D] (then the outputs [R][D]); the query rows [R][D]; the totals [R].
 template <bool EXACT>
@@ -348,40 +357,103 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rows_kernel(AttnParams a, i
     const float *vbase = a.vcache + a.layer_base + size_t(kv) * a.capacity * D;
     const int rows = min(R, n - z0);
     const int kblock = a.keys + z0 + rows - 1;  // keys of the block's last row, the most
-    // Passes 0 .. P - 1 stage keys, P .. 2P - 1 values, KC rows each: every thread's share (at most
-    // four float4s) of pass p + 1 is loaded into registers while pass p is worked on.
-    const int P = (kblock + KC - 1) / KC, D4 = D / 4;
-    float4 ahead[4];
+    // Passes 0 .. P - 1 stage keys, P .. 2P - 1 values, KC rows each: every thread's share of pass
+    // p + 1 is loaded into registers while pass p is worked on. A key pass takes matching float4s
+    // of a row's two halves (at most two pairs a thread) with their angles; a value pass at most four
+    // float4s.
+    const int P = (kblock + KC - 1) / KC, D4 = D / 4, D8 = D / 8, half = D / 2;
+    const int first = a.keys - 1;
+    const bool keeper = head % (a.heads / a.kv_heads) == 0;  // keeps this block's rows in the caches
+    const int keep_lo = first + z0, keep_hi = first + z0 + rows;
+    float *kkeep = a.kkeep + a.layer_base + size_t(kv) * a.capacity * D;
+    float *vkeep = a.vkeep + a.layer_base + size_t(kv) * a.capacity * D;
+    auto key_row = [&](int pos) {
+        return pos < first ? kbase + size_t(pos % a.capacity) * D : a.qkv + size_t(pos - first) * a.qkv_stride + size_t(a.heads + kv) * D;
+    };
+    auto value_row = [&](int pos) {
+        return pos < first ? vbase + size_t(pos % a.capacity) * D
+                           : a.qkv + size_t(pos - first) * a.qkv_stride + size_t(a.heads + a.kv_heads + kv) * D;
+    };
+    float4 ahead[4], cosv[2], sinv[2];
     auto load_pass = [&](int p) {
-        const float *base = p < P ? kbase : vbase;
-        const int c0 = (p < P ? p : p - P) * KC, nk = min(KC, kblock - c0);
+        if (p < P) {
+            const int c0 = p * KC, nk = min(KC, kblock - c0);
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int e = tid + k * kAttnThreads, row = e / D4;
-            if (row < nk) ahead[k] = *reinterpret_cast<const float4 *>(base + size_t((c0 + row) % a.capacity) * D + (e - row * D4) * 4);
+            for (int k = 0; k < 2; k++) {
+                const int e = tid + k * kAttnThreads, row = e / D8, c = (e - row * D8) * 4;
+                if (row >= nk) continue;
+                const int pos = c0 + row;
+                const float *src = key_row(pos);
+                ahead[2 * k] = *reinterpret_cast<const float4 *>(src + c);
+                ahead[2 * k + 1] = *reinterpret_cast<const float4 *>(src + half + c);
+                if (pos >= first) {
+                    cosv[k] = *reinterpret_cast<const float4 *>(a.rope + size_t(pos) * D + c);
+                    sinv[k] = *reinterpret_cast<const float4 *>(a.rope + size_t(pos) * D + half + c);
+                }
+            }
+        } else {
+            const int c0 = (p - P) * KC, nk = min(KC, kblock - c0);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int e = tid + k * kAttnThreads, row = e / D4;
+                if (row < nk) ahead[k] = *reinterpret_cast<const float4 *>(value_row(c0 + row) + (e - row * D4) * 4);
+            }
         }
     };
     auto store_pass = [&](int p) {
-        const int nk = min(KC, kblock - (p < P ? p : p - P) * KC);
+        if (p < P) {  // keys: rows D + 1 floats apart
+            const int c0 = p * KC, nk = min(KC, kblock - c0);
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int e = tid + k * kAttnThreads, row = e / D4;
-            if (row >= nk) continue;
-            if (p < P) {  // keys: rows D + 1 floats apart
-                float *dst = stage + row * S + (e - row * D4) * 4;
-                dst[0] = ahead[k].x;
-                dst[1] = ahead[k].y;
-                dst[2] = ahead[k].z;
-                dst[3] = ahead[k].w;
-            } else {
+            for (int k = 0; k < 2; k++) {
+                const int e = tid + k * kAttnThreads, row = e / D8, c = (e - row * D8) * 4;
+                if (row >= nk) continue;
+                const int pos = c0 + row;
+                float4 x = ahead[2 * k], y = ahead[2 * k + 1];
+                if (pos >= first) {  // the rotation by halves of rope_keep_rows_kernel
+                    const float4 cs = cosv[k], sn = sinv[k];
+                    const float4 nx = make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y, x.z * cs.z - y.z * sn.z,
+                                                  x.w * cs.w - y.w * sn.w);
+                    const float4 ny = make_float4(y.x * cs.x + x.x * sn.x, y.y * cs.y + x.y * sn.y, y.z * cs.z + x.z * sn.z,
+                                                  y.w * cs.w + x.w * sn.w);
+                    x = nx;
+                    y = ny;
+                    if (keeper && pos >= keep_lo && pos < keep_hi) {
+                        float *dst = kkeep + size_t(pos % a.capacity) * D;
+                        *reinterpret_cast<float4 *>(dst + c) = x;
+                        *reinterpret_cast<float4 *>(dst + half + c) = y;
+                    }
+                }
+                float *dst = stage + row * S + c;
+                dst[0] = x.x;
+                dst[1] = x.y;
+                dst[2] = x.z;
+                dst[3] = x.w;
+                dst[half] = y.x;
+                dst[half + 1] = y.y;
+                dst[half + 2] = y.z;
+                dst[half + 3] = y.w;
+            }
+        } else {
+            const int c0 = (p - P) * KC, nk = min(KC, kblock - c0);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int e = tid + k * kAttnThreads, row = e / D4;
+                if (row >= nk) continue;
                 reinterpret_cast<float4 *>(stage)[e] = ahead[k];
+                const int pos = c0 + row;
+                if (keeper && pos >= keep_lo && pos < keep_hi)
+                    *reinterpret_cast<float4 *>(vkeep + size_t(pos % a.capacity) * D + (e - row * D4) * 4) = ahead[k];
             }
         }
     };
     load_pass(0);
+    // the block's query rows, rotated at their own positions
     for (int e = tid; e < rows * D; e += kAttnThreads) {
-        const int r = e / D;
-        qrows[e] = a.qkv[size_t(z0 + r) * a.qkv_stride + size_t(head) * D + (e - r * D)];
+        const int r = e / D, d = e - r * D, j = d < half ? d : d - half;
+        const float *src = a.qkv + size_t(z0 + r) * a.qkv_stride + size_t(head) * D;
+        const float *cs = a.rope + size_t(first + z0 + r) * D;
+        const float c = cs[j], sn = cs[half + j], x = src[j], y = src[half + j];
+        qrows[e] = d < half ? x * c - y * sn : y * c + x * sn;
     }
     // scores (pairs key-fastest: neighbouring lanes read neighbouring key rows, D + 1 floats
     // apart, and one query row)
@@ -1125,12 +1197,8 @@ int prefill_layer(fg_qwen2 *m, size_t li, size_t first, int n, hipStream_t st)
     // prepare + QKV (layer/input.rs:22-66), rotary embeddings and the kept keys and values
     if ((rc = prefill_norm(m, ly.norm1, n, st))) return rc;
     if ((rc = prefill_product(m, ly.qkv, n, ly.qkv_bias, m->pre.qkv, qkv_w, false, st))) return rc;
-    rope_keep_rows_kernel<<<dim3(unsigned(n), unsigned(sh.heads + 2 * sh.kv_heads)), unsigned(sh.head_dim / 2), 0, st>>>(
-        m->pre.qkv, qkv_w, m->rope, int(sh.heads), int(sh.kv_heads), int(sh.head_dim), m->kcache, m->vcache, layer_base,
-        int(sh.capacity), int(first));
-    FG_HIP(hipGetLastError());
-    // attention of every row over the keys up to its own position (Mask::Causal), its output row
-    // quantized for the output projection
+    // rotary embeddings, the kept keys and values, and the attention of every row over the keys up
+    // to its own position (Mask::Causal), its output row quantized for the output projection
     AttnParams a{};
     a.qkv = m->pre.qkv;
     a.qkv_stride = qkv_w;
@@ -1150,12 +1218,20 @@ int prefill_layer(fg_qwen2 *m, size_t li, size_t first, int n, hipStream_t st)
     a.row_width = width;
     const int D = int(sh.head_dim), kmax = int(first) + n;
     if (const size_t rsmem = attn_rows_smem(D, kmax)) {
-        // blocks of rows sharing their keys and values (each row over its own keys)
+        // blocks of rows sharing their keys and values (each row over its own keys), the chunk's
+        // rows rotated and kept on the way
+        a.rope = m->rope;
+        a.kkeep = m->kcache;
+        a.vkeep = m->vcache;
         const int R = kAttnThreads / D;
         const dim3 rgrid(unsigned(sh.heads), unsigned((n + R - 1) / R));
         if (sh.exact) attn_rows_kernel<true><<<rgrid, kAttnThreads, rsmem, st>>>(a, n, (kmax + 3) / 4 * 4);
         else attn_rows_kernel<false><<<rgrid, kAttnThreads, rsmem, st>>>(a, n, (kmax + 3) / 4 * 4);
     } else {
+        rope_keep_rows_kernel<<<dim3(unsigned(n), unsigned(sh.heads + 2 * sh.kv_heads)), unsigned(sh.head_dim / 2), 0, st>>>(
+            m->pre.qkv, qkv_w, m->rope, int(sh.heads), int(sh.kv_heads), int(sh.head_dim), m->kcache, m->vcache, layer_base,
+            int(sh.capacity), int(first));
+        FG_HIP(hipGetLastError());
         const dim3 sgrid(unsigned(sh.kv_heads), unsigned((first + n + kScoreKeys - 1) / kScoreKeys), unsigned(n));
         attn_scores_kernel<<<sgrid, kAttnThreads, m->score_smem, st>>>(a);
         FG_HIP(hipGetLastError());

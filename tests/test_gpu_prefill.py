@@ -121,7 +121,7 @@ def test_read_head_sizes(fk, head_dim, heads, kv_heads):
     assert rel_l2(got[0], want[0]) < FAST_TOLERANCE and rel_l2(got[1], want[1]) < FAST_TOLERANCE
 
 
-@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
 def test_qwen2_half_billion_shape_prefill_of_158_rows(fk, dtype):
     """The Qwen2-0.5B shape: 158 rows from position 100 (a cache of N(0,1) rows before it) in chunks
     of 64, the reference's prefill length (models/ming/baseline.json:52-55): bit-identical."""

@@ -268,11 +268,11 @@ def test_decoder_rejects_positions_past_the_cache(fk):
 
 
 @pytest.mark.parametrize("exact", [True, False])
-@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q4B32])
+@pytest.mark.parametrize("dtype", [O.Q7B32, O.Q8B32, O.Q4B32])
 def test_qwen2_half_billion_shape_at_position_511(fk, exact, dtype):
     """The Qwen2-0.5B-shaped step (hidden 896, 24 layers, 14/2 heads of 64, FFN 4864, vocabulary
-    151936) at position 511 over a cache of N(0,1) keys and values, with 7-bit and 4-bit tables
-    (the reference's LM layers run Q4b32: models/ming/compile/src/lib.rs:49-56)."""
+    151936) at position 511 over a cache of N(0,1) keys and values, with 7-bit, full-range 8-bit
+    and 4-bit tables (the reference's LM layers run Q4b32: models/ming/compile/src/lib.rs:49-56)."""
     print(f"Qwen2-0.5B shape dtype {dtype} exact {exact}", flush=True)
     params = build(dtype, hidden=896, layers=24, heads=14, kv_heads=2, head_dim=64, ffn=4864, vocab=151936,
                    capacity=512, seed=11, synthetic=True)
